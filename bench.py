@@ -1,0 +1,191 @@
+"""Sampler benchmark: sampled rows/s and HBM GB/s on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload mixed128k]
+
+A step is one batched sampling pass over one batch held in HBM (default
+mixed128k: 256 rows x 128256 fp32 logits, mixed per-row parameters, see
+pagellm_amd/workloads.py).  Three copies of the logits rotate across steps
+(3 x 131 MB > the 256 MB Infinity Cache), so every step streams from HBM.
+The K timed steps are bracketed by HIP events recorded on the stream the
+kernels are launched on.  Rank 0 prints one JSON line.
+
+The CPU baseline is the numpy oracle looping over rows like the reference
+engine (llm_engine.py:238-254), one pinned core with BLAS threads pinned to
+1, on a bounded sample of the same workload, in a child process that never
+touches the GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBPS = 8000.0
+METRIC = "sampled rows/sec + HBM GB/s (% peak), batch 256 × vocab 128256 fp32"
+
+
+def cpu_baseline_child(workload: str, rows: int, reps: int) -> None:
+    """Runs in a fresh process: 1 pinned core, BLAS pinned to 1 thread."""
+    cores = sorted(os.sched_getaffinity(0))
+    os.sched_setaffinity(0, {cores[0]})
+    import numpy as np
+
+    import oracle
+    from pagellm_amd import workloads
+
+    w = workloads.WORKLOADS[workload]()
+    B = w["logits"].shape[0]
+    sel = np.linspace(0, B - 1, min(rows, B)).astype(int)
+    x = w["logits"][sel]
+    params = [w["params"][i] for i in sel]
+    u = w["uniforms"][sel]
+    ctx = [w["contexts"][i] for i in sel]
+    oracle.sample_batch(x[:2], params[:2], u[:2], ctx[:2])  # warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        oracle.sample_batch(x, params, u, ctx)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    print(json.dumps({
+        "value": len(sel) / med, "unit": "rows/s", "cores": 1, "kind": "port",
+        "sample": f"{len(sel)} of {B} {workload} rows (evenly spaced, all parameter groups), "
+                  f"median of {reps} reps of {med:.2f} s, numpy {np.__version__}, "
+                  f"host cpus {os.cpu_count()}",
+    }))
+
+
+def run_cpu_baseline(workload: str, rows: int, reps: int):
+    env = dict(os.environ, OMP_NUM_THREADS="1", OPENBLAS_NUM_THREADS="1", MKL_NUM_THREADS="1",
+               HIP_VISIBLE_DEVICES="", CUDA_VISIBLE_DEVICES="")
+    r = subprocess.run([sys.executable, str(Path(__file__).resolve()), "--cpu-baseline-child", "--workload", workload,
+                        "--cpu-rows", str(rows), "--cpu-reps", str(reps)],
+                       capture_output=True, text=True, env=env, timeout=900)
+    if r.returncode != 0:
+        sys.stderr.write(r.stderr)
+        return None
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def load_traffic(workload: str):
+    f = ROOT / "profiles" / f"traffic_{workload}.json"
+    if f.exists():
+        try:
+            return json.loads(f.read_text()).get("bytes_per_launch")
+        except Exception:
+            return None
+    return None
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="mixed128k", choices=["mixed128k", "zipf32k", "zipf152k", "char65"])
+    ap.add_argument("--sets", type=int, default=3, help="rotating input copies")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=256)
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--cpu-baseline-child", action="store_true")
+    args = ap.parse_args()
+
+    if args.cpu_baseline_child:
+        cpu_baseline_child(args.workload, args.cpu_rows, args.cpu_reps)
+        return
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(rows shard across GPUs with no exchange; see the sharding notes in the design document)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from pagellm_amd import _native, workloads
+    from pagellm_amd.sampling import _pack_histories, _pack_params
+
+    print(f"[bench] generating {args.workload}", file=sys.stderr, flush=True)
+    w = workloads.WORKLOADS[args.workload]()
+    B, V = w["logits"].shape
+    algo_bytes = workloads.algorithmic_bytes(w)
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)
+    ctx = _native.Context(0)
+    ctx.set_stream(stream.cuda_stream)
+    torch.cuda.set_stream(stream)
+
+    t, k, p, r = _pack_params(w["params"])
+    hist_ids, hist_off = _pack_histories(w["contexts"], w["params"], B, V)
+    logits = [torch.from_numpy(w["logits"]).to(dev) for _ in range(args.sets)]
+    d = {n: torch.from_numpy(a).to(dev) for n, a in
+         dict(t=t, k=k, p=p, r=r, u=w["uniforms"], ids=hist_ids, off=hist_off).items() if a is not None}
+    out = torch.empty(B, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+
+    def step(i):
+        x = logits[i % args.sets]
+        ctx.sample(x.data_ptr(), _native.PLH_F32, V, B, V,
+                   d["ids"].data_ptr() if "ids" in d else None, d["off"].data_ptr() if "off" in d else None,
+                   d["t"].data_ptr(), d["k"].data_ptr(), d["p"].data_ptr(), d["r"].data_ptr(),
+                   d["u"].data_ptr(), out.data_ptr(), None, 0)
+
+    fb0 = ctx.fallback_rows()
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(args.steps):
+        step(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    fallback = (ctx.fallback_rows() - fb0) / max(1, args.warmup + args.steps)
+
+    ids = out.cpu().numpy()
+    greedy = [i for i, pp in enumerate(w["params"]) if pp.greedy]
+    if greedy and not np.array_equal(ids[greedy], np.argmax(w["logits"][greedy], axis=1)):
+        print("[bench] WARNING: greedy rows disagree with numpy argmax", file=sys.stderr)
+
+    rows_per_s = B / (ms * 1e-3)
+    gbps = algo_bytes / (ms * 1e-3) / 1e9
+    cpu = None if args.no_cpu_baseline else run_cpu_baseline(args.workload, args.cpu_rows, args.cpu_reps)
+    res = {
+        "metric": METRIC,
+        "value": rows_per_s,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic",
+        "config": {"workload": args.workload, "batch": B, "vocab": V, "logits_dtype": "fp32",
+                   "rotating_input_sets": args.sets, "algorithmic_bytes_per_step": algo_bytes},
+        "hbm_gbps": gbps,
+        "hbm_frac": gbps / PEAK_HBM_GBPS,
+        "fallback_rows_per_step": fallback,
+        "roofline": {"bound": "hbm", "achieved": gbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": gbps / PEAK_HBM_GBPS, "traffic": load_traffic(args.workload),
+                     "kernel": "k_sample_split"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,142 @@
+/*
+ * pagellm_hip.h - C ABI of libpagellm_hip.so, the MI355X (gfx950) sampler
+ * for pagellm.
+ *
+ * Plain C types only: every tensor argument is a device pointer (from
+ * plh_alloc, hipMalloc, or a torch tensor's data_ptr()) plus explicit sizes.
+ * Every function returns PLH_OK (0) or a negative PLH_ERR_* code; the
+ * message of the last failure on a context is available from
+ * plh_last_error().  No C++ exception or abort() crosses this boundary.
+ *
+ * Threading: a plh_ctx is not thread-safe.  Use one context per host thread
+ * (the reference samples from its single engine thread,
+ * docs/adr/0004-single-engine-thread.md).  Work is queued on the context's
+ * stream; plh_sync() waits for it.
+ *
+ * Randomness never comes from the device: callers pass uniforms in [0, 1)
+ * drawn on the host from each sequence's numpy Generator
+ * (src/pagellm/engine/sampling.py:110-111), in the reference's order.
+ */
+#ifndef PAGELLM_HIP_H
+#define PAGELLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PLH_ABI_VERSION 1
+
+/* status codes */
+#define PLH_OK 0
+#define PLH_ERR_INVALID_ARG -1
+#define PLH_ERR_HIP -2
+#define PLH_ERR_OUT_OF_MEMORY -3
+#define PLH_ERR_UNSUPPORTED -4
+#define PLH_ERR_NO_DEVICE -5
+
+/* element types of logits / probability inputs */
+#define PLH_F32 0
+#define PLH_F64 1
+
+/* plh_sample flags */
+#define PLH_SAMPLE_ROWWISE 1 /* one workgroup per row (the general kernel) */
+
+/* plh_set_option options */
+#define PLH_OPT_TOPP_CAP 1 /* candidates kept per 8192-token chunk for top-p rows, 16..8192 (default 640) */
+
+typedef struct plh_ctx plh_ctx;
+
+/* Version of this ABI (PLH_ABI_VERSION). */
+int plh_abi_version(void);
+
+/* Context on HIP device `device`, with its own stream.  No reference
+ * counterpart: the reference samples on the host (sampling.py). */
+int plh_create(plh_ctx** out, int device);
+void plh_destroy(plh_ctx* ctx);
+const char* plh_last_error(const plh_ctx* ctx);
+/* Queue work on `stream` (a hipStream_t, e.g. torch's current stream); NULL
+ * restores the context's own stream. */
+int plh_set_stream(plh_ctx* ctx, void* stream);
+int plh_set_option(plh_ctx* ctx, int option, int64_t value);
+/* Rows finished by the general row-wise pipeline inside the fast kernel,
+ * cumulative since plh_create (waits for queued work). */
+int plh_fallback_rows(plh_ctx* ctx, int64_t* out);
+
+/* Device memory helpers so numpy callers need no other GPU library.
+ * plh_h2d / plh_d2h return once the copy is complete. */
+int plh_alloc(plh_ctx* ctx, void** out, size_t bytes);
+int plh_free(plh_ctx* ctx, void* ptr);
+int plh_h2d(plh_ctx* ctx, void* dst, const void* src, size_t bytes);
+int plh_d2h(plh_ctx* ctx, void* dst, const void* src, size_t bytes);
+int plh_sync(plh_ctx* ctx);
+
+/*
+ * Batched sample(): replaces the per-sequence loop of
+ * src/pagellm/engine/llm_engine.py:238-254 over
+ * src/pagellm/engine/sampling.py:101-107 (sample), :65-91 (probs),
+ * :94-98 (draw), :52-62 (apply_repetition_penalty).
+ *
+ *   logits      [B, ld] of `dtype` (PLH_F32 / PLH_F64); row b starts at b*ld
+ *   hist_ids    int32 token ids, CSR over rows (the sequence's full history,
+ *               prompt + outputs, llm_engine.py:283); may be NULL with
+ *   hist_off    int64 [B+1] offsets into hist_ids, or NULL (no history)
+ *   temperature float64 [B]  0 => greedy (SamplingParams.greedy, :47-49)
+ *   top_k       int32 [B]    0 or >= V => disabled
+ *   top_p       float64 [B]  1 => disabled
+ *   rep_penalty float64 [B]  1 => disabled
+ *   uniforms    float64 [B]  one uniform per non-greedy row (rng.random()
+ *               of :98); ignored for greedy rows
+ *   out_ids     int32 [B]    sampled token ids
+ *   out_probs   float64 [B, V] or NULL: when given, the processed
+ *               distribution (probs(), :65-91) is written too and the
+ *               row-wise kernel is used
+ *   flags       PLH_SAMPLE_* bits
+ * Histories with an active penalty require V <= 262144.
+ */
+int plh_sample(plh_ctx* ctx, const void* logits, int dtype, int64_t ld, int B, int V,
+               const int32_t* hist_ids, const int64_t* hist_off, const double* temperature,
+               const int32_t* top_k, const double* top_p, const double* rep_penalty,
+               const double* uniforms, int32_t* out_ids, double* out_probs, int flags);
+
+/*
+ * apply_repetition_penalty() on a copy: src/pagellm/engine/sampling.py:52-62.
+ * out[b, :V] = x[b, :V] with every distinct id of row b's history mapped
+ * through x > 0 ? x / penalty : x * penalty, computed in `dtype`.
+ */
+int plh_penalize(plh_ctx* ctx, const void* x, int dtype, int64_t ld, int B, int V,
+                 const int32_t* hist_ids, const int64_t* hist_off, const double* rep_penalty,
+                 void* out, int64_t out_ld);
+
+/*
+ * draw(): src/pagellm/engine/sampling.py:94-98 for B rows of non-negative
+ * weights p[b, :V] (any scale): first i with cumsum(p)[i] > u[b] * sum(p),
+ * else V-1.
+ */
+int plh_draw(plh_ctx* ctx, const void* p, int dtype, int64_t ld, int B, int V,
+             const double* uniforms, int32_t* out_ids);
+
+/*
+ * Batched verify(): src/pagellm/engine/speculative.py:38-60.
+ *   p           [B, k+1, V] target distributions (dtype)
+ *   q           [B, k, V] draft distributions (dtype)
+ *   draft       int32 [B, k] proposed tokens (0 <= id < V)
+ *   accept_u    float64 [B, k]: test i accepts while accept_u < min(1, p/q)
+ *   draw_u      float64 [B] (draw_u_per_stop = 0) or [B, k+1] (= 1, the
+ *               uniform used when the walk stops at position s is
+ *               draw_u[b, s])
+ *   out_tokens  int32 [B, k+1]: accepted drafts, then the residual or bonus
+ *               token, then -1 padding
+ *   out_n_acc   int32 [B]: accepted draft count
+ */
+int plh_verify(plh_ctx* ctx, const void* p, const void* q, int dtype, int B, int k, int V,
+               const int32_t* draft, const double* accept_u, const double* draw_u,
+               int draw_u_per_stop, int32_t* out_tokens, int32_t* out_n_acc);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGELLM_HIP_H */

@@ -1,0 +1,328 @@
+// C ABI of libpagellm_hip.so (declared in include/pagellm_hip.h): context,
+// device memory helpers, argument validation and kernel launches.
+#include <stdio.h>
+#include <string.h>
+
+#include <new>
+#include <string>
+
+#include "../../include/pagellm_hip.h"
+#include "plh_kernels.h"
+
+struct plh_ctx {
+  int device = 0;
+  hipStream_t own_stream = nullptr;
+  hipStream_t stream = nullptr;
+  // split-kernel workspace
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  uint32_t* row_count = nullptr;  // separate: must stay zero between launches
+  size_t row_count_n = 0;
+  unsigned long long* fallback = nullptr;
+  int topp_cap = 640;
+  std::string err;
+};
+
+namespace {
+
+constexpr int kMaxVBitmap = 262144;
+constexpr int kMaxSplitChunks = 256;
+
+int fail(plh_ctx* c, int code, const char* fmt, const char* detail = nullptr) {
+  if (c != nullptr) {
+    char buf[512];
+    snprintf(buf, sizeof(buf), fmt, detail != nullptr ? detail : "");
+    c->err = buf;
+  }
+  return code;
+}
+
+int hip_fail(plh_ctx* c, hipError_t e, const char* where) {
+  if (c != nullptr) {
+    c->err = std::string(where) + ": " + hipGetErrorString(e);
+  }
+  return e == hipErrorOutOfMemory ? PLH_ERR_OUT_OF_MEMORY : PLH_ERR_HIP;
+}
+
+#define PLH_HIP(ctx, call, where)                   \
+  do {                                              \
+    hipError_t e_ = (call);                         \
+    if (e_ != hipSuccess) return hip_fail(ctx, e_, where); \
+  } while (0)
+
+int use_device(plh_ctx* c) {
+  if (c == nullptr) return PLH_ERR_INVALID_ARG;
+  PLH_HIP(c, hipSetDevice(c->device), "hipSetDevice");
+  return PLH_OK;
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+int ensure_workspace(plh_ctx* c, int B, int G, int cap, plh::SampleArgs& a) {
+  const size_t nchunks = (size_t)B * G;
+  const size_t sums = align_up(nchunks * sizeof(plh::ChunkSum), 256);
+  const size_t ncand = nchunks * (size_t)cap;
+  const size_t cz = align_up(ncand * sizeof(double), 256);
+  const size_t cidx = align_up(ncand * sizeof(int32_t), 256);
+  const size_t cp = cz;
+  const size_t need = sums + cz + cidx + cp;
+  if (need > c->ws_bytes) {
+    if (c->ws != nullptr) {
+      PLH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+      PLH_HIP(c, hipFree(c->ws), "hipFree");
+      c->ws = nullptr;
+      c->ws_bytes = 0;
+    }
+    PLH_HIP(c, hipMalloc(&c->ws, need), "hipMalloc(workspace)");
+    c->ws_bytes = need;
+  }
+  if ((size_t)B > c->row_count_n) {
+    if (c->row_count != nullptr) {
+      PLH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+      PLH_HIP(c, hipFree(c->row_count), "hipFree");
+      c->row_count = nullptr;
+      c->row_count_n = 0;
+    }
+    const size_t n = B < 1024 ? 1024 : (size_t)B;
+    PLH_HIP(c, hipMalloc(&c->row_count, n * sizeof(uint32_t)), "hipMalloc(row counters)");
+    PLH_HIP(c, hipMemsetAsync(c->row_count, 0, n * sizeof(uint32_t), c->stream), "hipMemsetAsync");
+    c->row_count_n = n;
+  }
+  char* base = static_cast<char*>(c->ws);
+  a.sums = reinterpret_cast<plh::ChunkSum*>(base);
+  a.cz = reinterpret_cast<double*>(base + sums);
+  a.cidx = reinterpret_cast<int32_t*>(base + sums + cz);
+  a.cp = reinterpret_cast<double*>(base + sums + cz + cidx);
+  a.row_count = c->row_count;
+  a.fallback_rows = c->fallback;
+  return PLH_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int plh_abi_version(void) { return PLH_ABI_VERSION; }
+
+int plh_create(plh_ctx** out, int device) {
+  if (out == nullptr) return PLH_ERR_INVALID_ARG;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return PLH_ERR_NO_DEVICE;
+  if (device < 0 || device >= n) return PLH_ERR_INVALID_ARG;
+  plh_ctx* c = new (std::nothrow) plh_ctx();
+  if (c == nullptr) return PLH_ERR_OUT_OF_MEMORY;
+  c->device = device;
+  int rc = PLH_OK;
+  do {
+    if (hipSetDevice(device) != hipSuccess) { rc = PLH_ERR_HIP; break; }
+    if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess) { rc = PLH_ERR_HIP; break; }
+    c->stream = c->own_stream;
+    if (hipMalloc(&c->fallback, sizeof(unsigned long long)) != hipSuccess) { rc = PLH_ERR_OUT_OF_MEMORY; break; }
+    if (hipMemset(c->fallback, 0, sizeof(unsigned long long)) != hipSuccess) { rc = PLH_ERR_HIP; break; }
+  } while (0);
+  if (rc != PLH_OK) {
+    plh_destroy(c);
+    return rc;
+  }
+  *out = c;
+  return PLH_OK;
+}
+
+void plh_destroy(plh_ctx* c) {
+  if (c == nullptr) return;
+  (void)hipSetDevice(c->device);
+  if (c->stream != nullptr) (void)hipStreamSynchronize(c->stream);
+  if (c->ws != nullptr) (void)hipFree(c->ws);
+  if (c->row_count != nullptr) (void)hipFree(c->row_count);
+  if (c->fallback != nullptr) (void)hipFree(c->fallback);
+  if (c->own_stream != nullptr) (void)hipStreamDestroy(c->own_stream);
+  delete c;
+}
+
+const char* plh_last_error(const plh_ctx* c) { return c == nullptr ? "null context" : c->err.c_str(); }
+
+int plh_set_stream(plh_ctx* c, void* stream) {
+  if (c == nullptr) return PLH_ERR_INVALID_ARG;
+  c->stream = stream != nullptr ? static_cast<hipStream_t>(stream) : c->own_stream;
+  return PLH_OK;
+}
+
+int plh_set_option(plh_ctx* c, int option, int64_t value) {
+  if (c == nullptr) return PLH_ERR_INVALID_ARG;
+  switch (option) {
+    case PLH_OPT_TOPP_CAP:
+      if (value < 16 || value > plh::kChunk) return fail(c, PLH_ERR_INVALID_ARG, "PLH_OPT_TOPP_CAP must be in [16, 8192]%s");
+      c->topp_cap = (int)value;
+      return PLH_OK;
+    default:
+      return fail(c, PLH_ERR_INVALID_ARG, "unknown option%s");
+  }
+}
+
+int plh_fallback_rows(plh_ctx* c, int64_t* out) {
+  if (c == nullptr || out == nullptr) return PLH_ERR_INVALID_ARG;
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  unsigned long long v = 0;
+  PLH_HIP(c, hipMemcpyAsync(&v, c->fallback, sizeof(v), hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync");
+  PLH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  *out = (int64_t)v;
+  return PLH_OK;
+}
+
+int plh_alloc(plh_ctx* c, void** out, size_t bytes) {
+  if (c == nullptr || out == nullptr) return PLH_ERR_INVALID_ARG;
+  *out = nullptr;
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  if (bytes == 0) bytes = 1;
+  PLH_HIP(c, hipMalloc(out, bytes), "hipMalloc");
+  return PLH_OK;
+}
+
+int plh_free(plh_ctx* c, void* p) {
+  if (c == nullptr) return PLH_ERR_INVALID_ARG;
+  if (p == nullptr) return PLH_OK;
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  PLH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  PLH_HIP(c, hipFree(p), "hipFree");
+  return PLH_OK;
+}
+
+int plh_h2d(plh_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (c == nullptr || (bytes > 0 && (dst == nullptr || src == nullptr))) return PLH_ERR_INVALID_ARG;
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  if (bytes == 0) return PLH_OK;
+  PLH_HIP(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(H2D)");
+  PLH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  return PLH_OK;
+}
+
+int plh_d2h(plh_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (c == nullptr || (bytes > 0 && (dst == nullptr || src == nullptr))) return PLH_ERR_INVALID_ARG;
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  if (bytes == 0) return PLH_OK;
+  PLH_HIP(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync(D2H)");
+  PLH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  return PLH_OK;
+}
+
+int plh_sync(plh_ctx* c) {
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  PLH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  return PLH_OK;
+}
+
+int plh_sample(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, int V, const int32_t* hist_ids,
+               const int64_t* hist_off, const double* temperature, const int32_t* top_k, const double* top_p,
+               const double* rep_penalty, const double* uniforms, int32_t* out_ids, double* out_probs,
+               int flags) {
+  if (c == nullptr) return PLH_ERR_INVALID_ARG;
+  if (B < 0 || V < 1) return fail(c, PLH_ERR_INVALID_ARG, "need B >= 0 and V >= 1%s");
+  if (B == 0) return PLH_OK;
+  if (dtype != PLH_F32 && dtype != PLH_F64) return fail(c, PLH_ERR_INVALID_ARG, "dtype must be PLH_F32 or PLH_F64%s");
+  if (ld < V) return fail(c, PLH_ERR_INVALID_ARG, "ld must be >= V%s");
+  if (logits == nullptr || temperature == nullptr || top_k == nullptr || top_p == nullptr ||
+      rep_penalty == nullptr || out_ids == nullptr)
+    return fail(c, PLH_ERR_INVALID_ARG, "null device pointer%s");
+  if (hist_off != nullptr && hist_ids == nullptr)
+    return fail(c, PLH_ERR_INVALID_ARG, "hist_off given without hist_ids%s");
+  if (hist_off != nullptr && V > kMaxVBitmap)
+    return fail(c, PLH_ERR_UNSUPPORTED, "repetition-penalty histories need V <= 262144%s");
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  const size_t esize = dtype == PLH_F64 ? 8 : 4;
+  const bool vec = aligned16(logits) && ((size_t)ld * esize) % 16 == 0;
+  plh::SampleArgs a{};
+  a.logits = logits;
+  a.ld = ld;
+  a.B = B;
+  a.V = V;
+  a.hist_ids = hist_ids;
+  a.hist_off = hist_off;
+  a.temperature = temperature;
+  a.top_k = top_k;
+  a.top_p = top_p;
+  a.rep_penalty = rep_penalty;
+  a.uniforms = uniforms;
+  a.out_ids = out_ids;
+  a.out_probs = out_probs;
+  const int G = (V + plh::kChunk - 1) / plh::kChunk;
+  hipError_t e;
+  if (out_probs != nullptr || (flags & PLH_SAMPLE_ROWWISE) || G > kMaxSplitChunks) {
+    e = plh::launch_sample_rows(a, dtype == PLH_F64, vec, c->stream);
+  } else {
+    a.G = G;
+    a.cap = c->topp_cap;
+    a.xcd_map = B >= 8 ? 1 : 0;
+    rc = ensure_workspace(c, B, G, a.cap, a);
+    if (rc != PLH_OK) return rc;
+    e = plh::launch_sample_split(a, dtype == PLH_F64, vec, c->stream);
+  }
+  if (e != hipSuccess) return hip_fail(c, e, "plh_sample launch");
+  return PLH_OK;
+}
+
+int plh_penalize(plh_ctx* c, const void* x, int dtype, int64_t ld, int B, int V, const int32_t* hist_ids,
+                 const int64_t* hist_off, const double* rep_penalty, void* out, int64_t out_ld) {
+  if (c == nullptr) return PLH_ERR_INVALID_ARG;
+  if (B < 0 || V < 1) return fail(c, PLH_ERR_INVALID_ARG, "need B >= 0 and V >= 1%s");
+  if (B == 0) return PLH_OK;
+  if (dtype != PLH_F32 && dtype != PLH_F64) return fail(c, PLH_ERR_INVALID_ARG, "dtype must be PLH_F32 or PLH_F64%s");
+  if (ld < V || out_ld < V) return fail(c, PLH_ERR_INVALID_ARG, "ld and out_ld must be >= V%s");
+  if (x == nullptr || out == nullptr || rep_penalty == nullptr)
+    return fail(c, PLH_ERR_INVALID_ARG, "null device pointer%s");
+  if (hist_off != nullptr && hist_ids == nullptr)
+    return fail(c, PLH_ERR_INVALID_ARG, "hist_off given without hist_ids%s");
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  plh::PenalizeArgs a{x, ld, out, out_ld, B, V, hist_ids, hist_off, rep_penalty};
+  const hipError_t e = plh::launch_penalize(a, dtype == PLH_F64, c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "plh_penalize launch");
+  return PLH_OK;
+}
+
+int plh_draw(plh_ctx* c, const void* p, int dtype, int64_t ld, int B, int V, const double* uniforms,
+             int32_t* out_ids) {
+  if (c == nullptr) return PLH_ERR_INVALID_ARG;
+  if (B < 0 || V < 1) return fail(c, PLH_ERR_INVALID_ARG, "need B >= 0 and V >= 1%s");
+  if (B == 0) return PLH_OK;
+  if (dtype != PLH_F32 && dtype != PLH_F64) return fail(c, PLH_ERR_INVALID_ARG, "dtype must be PLH_F32 or PLH_F64%s");
+  if (ld < V) return fail(c, PLH_ERR_INVALID_ARG, "ld must be >= V%s");
+  if (p == nullptr || uniforms == nullptr || out_ids == nullptr)
+    return fail(c, PLH_ERR_INVALID_ARG, "null device pointer%s");
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  plh::DrawArgs a{p, ld, B, V, uniforms, out_ids};
+  const hipError_t e = plh::launch_draw(a, dtype == PLH_F64, c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "plh_draw launch");
+  return PLH_OK;
+}
+
+int plh_verify(plh_ctx* c, const void* p, const void* q, int dtype, int B, int k, int V, const int32_t* draft,
+               const double* accept_u, const double* draw_u, int draw_u_per_stop, int32_t* out_tokens,
+               int32_t* out_n_acc) {
+  if (c == nullptr) return PLH_ERR_INVALID_ARG;
+  if (B < 0 || k < 0 || V < 1) return fail(c, PLH_ERR_INVALID_ARG, "need B >= 0, k >= 0 and V >= 1%s");
+  if (B == 0) return PLH_OK;
+  if (dtype != PLH_F32 && dtype != PLH_F64) return fail(c, PLH_ERR_INVALID_ARG, "dtype must be PLH_F32 or PLH_F64%s");
+  if (p == nullptr || draw_u == nullptr || out_tokens == nullptr || out_n_acc == nullptr)
+    return fail(c, PLH_ERR_INVALID_ARG, "null device pointer%s");
+  if (k > 0 && (q == nullptr || draft == nullptr || accept_u == nullptr))
+    return fail(c, PLH_ERR_INVALID_ARG, "null device pointer%s");
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  plh::VerifyArgs a{p, q, B, k, V, draft, accept_u, draw_u, draw_u_per_stop ? 1 : 0, out_tokens, out_n_acc};
+  const hipError_t e = plh::launch_verify(a, dtype == PLH_F64, c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "plh_verify launch");
+  return PLH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,213 @@
+// Device primitives shared by the gfx950 sampler kernels: order-preserving
+// keys, fixed-point masses, wave64/workgroup reductions and scans.
+//
+// Every reduction and scan here combines values in a fixed order (xor
+// butterflies inside a wave, then the waves' partials left to right), so the
+// kernels are deterministic run to run.  Integer (fixed-point) scans are
+// exact, which is what the inverse-CDF draws and the top-p mass selection
+// rely on.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace plh {
+
+constexpr int kWave = 64;
+constexpr int kThreads = 512;  // every kernel in this library runs 8 waves of 64
+constexpr int kWaves = kThreads / kWave;
+
+// 2^62: probabilities (each <= 1, sum ~1) become exact-addable integers.
+constexpr double kFxScale = 4611686018427387904.0;
+
+__device__ __forceinline__ int lane() { return threadIdx.x & (kWave - 1); }
+__device__ __forceinline__ int wave() { return threadIdx.x >> 6; }
+
+// Larger double -> larger key; -0.0 and +0.0 share a key (numpy compares them
+// equal).  NaN is outside the supported input domain.
+__device__ __forceinline__ uint64_t key_of(double d) {
+  d = d + 0.0;
+  const uint64_t u = (uint64_t)__double_as_longlong(d);
+  return (u >> 63) ? ~u : (u | 0x8000000000000000ull);
+}
+
+__device__ __forceinline__ double val_of_key(uint64_t k) {
+  const uint64_t u = (k >> 63) ? (k & 0x7fffffffffffffffull) : ~k;
+  return __longlong_as_double((long long)u);
+}
+
+// Coarse 32-bit key: the order key of z rounded toward -inf to float.  It is
+// monotone non-decreasing in z, and key32(a) < key32(b) implies a < b.
+__device__ __forceinline__ uint32_t key32_of(double d) {
+  float f = __double2float_rd(d);
+  f = f + 0.0f;
+  const uint32_t u = __float_as_uint(f);
+  return (u >> 31) ? ~u : (u | 0x80000000u);
+}
+
+// Bits of a non-negative double are already order preserving.
+__device__ __forceinline__ uint64_t pkey_of(double p) { return (uint64_t)__double_as_longlong(p + 0.0); }
+
+__device__ __forceinline__ uint64_t to_fx(double p) {
+  return p > 0.0 ? (uint64_t)__double2ull_rn(p * kFxScale) : 0ull;
+}
+
+// Largest double strictly below d (d finite).
+__device__ __forceinline__ double dbl_prev(double d) {
+  if (d == 0.0) return -4.9406564584124654e-324;
+  const long long u = __double_as_longlong(d);
+  return __longlong_as_double(d > 0.0 ? u - 1 : u + 1);
+}
+
+// ---------------------------------------------------------- LDS atomics
+// Explicit address-space-3 atomics for workgroup-shared counters and
+// histograms: they lower to ds_* instructions, never to flat atomics.
+#define PLH_LDS(T, p) ((__attribute__((address_space(3))) T*)(p))
+
+__device__ __forceinline__ void lds_add(uint32_t* p, uint32_t v) {
+  __hip_atomic_fetch_add(PLH_LDS(uint32_t, p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_add(uint64_t* p, uint64_t v) {
+  __hip_atomic_fetch_add(PLH_LDS(uint64_t, p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ int lds_fetch_add(int* p, int v) {
+  return __hip_atomic_fetch_add(PLH_LDS(int, p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_or(uint32_t* p, uint32_t v) {
+  __hip_atomic_fetch_or(PLH_LDS(uint32_t, p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_min(int* p, int v) {
+  __hip_atomic_fetch_min(PLH_LDS(int, p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Device-wide counters in global memory (address space 1), agent scope.
+#define PLH_GLB(T, p) ((__attribute__((address_space(1))) T*)(p))
+
+__device__ __forceinline__ uint32_t glb_fetch_add(uint32_t* p, uint32_t v) {
+  return __hip_atomic_fetch_add(PLH_GLB(uint32_t, p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void glb_add(unsigned long long* p, unsigned long long v) {
+  __hip_atomic_fetch_add(PLH_GLB(unsigned long long, p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ------------------------------------------------------------ reductions
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_max(T v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const T o = __shfl_xor(v, off);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_min(T v) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const T o = __shfl_xor(v, off);
+    v = o < v ? o : v;
+  }
+  return v;
+}
+
+// All threads of the workgroup receive the result.  `red` holds kWaves slots.
+template <typename T>
+__device__ __forceinline__ T block_sum(T v, T* red) {
+  v = wave_sum(v);
+  if (lane() == 0) red[wave()] = v;
+  __syncthreads();
+  T r = red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) r += red[w];
+  __syncthreads();
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ T block_max(T v, T* red) {
+  v = wave_max(v);
+  if (lane() == 0) red[wave()] = v;
+  __syncthreads();
+  T r = red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) r = red[w] > r ? red[w] : r;
+  __syncthreads();
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ T block_min(T v, T* red) {
+  v = wave_min(v);
+  if (lane() == 0) red[wave()] = v;
+  __syncthreads();
+  T r = red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) r = red[w] < r ? red[w] : r;
+  __syncthreads();
+  return r;
+}
+
+// (value, index) maximum; ties go to the lowest index, as numpy's argmax.
+struct ArgMax {
+  double v;
+  int i;
+};
+
+__device__ __forceinline__ ArgMax argmax_merge(ArgMax a, ArgMax b) {
+  return (b.v > a.v || (b.v == a.v && b.i < a.i)) ? b : a;
+}
+
+__device__ __forceinline__ ArgMax block_argmax(ArgMax a, double* redd, int* redi) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    ArgMax o;
+    o.v = __shfl_xor(a.v, off);
+    o.i = __shfl_xor(a.i, off);
+    a = argmax_merge(a, o);
+  }
+  if (lane() == 0) {
+    redd[wave()] = a.v;
+    redi[wave()] = a.i;
+  }
+  __syncthreads();
+  ArgMax r{redd[0], redi[0]};
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) r = argmax_merge(r, ArgMax{redd[w], redi[w]});
+  __syncthreads();
+  return r;
+}
+
+// Exclusive scan of one unsigned integer per thread in thread order; *total
+// receives the sum over the workgroup.  Exact.
+template <typename T>
+__device__ __forceinline__ T block_excl_scan(T v, T* red, T* total) {
+  T x = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const T y = __shfl_up(x, off);
+    if (lane() >= off) x += y;
+  }
+  if (lane() == kWave - 1) red[wave()] = x;
+  __syncthreads();
+  T pre = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const T s = red[w];
+    if (w < wave()) pre += s;
+    tot += s;
+  }
+  __syncthreads();
+  *total = tot;
+  return pre + (x - v);
+}
+
+}  // namespace plh

@@ -1,0 +1,108 @@
+"""GPU parity of speculative verify against the CPU oracle (needs an MI355X):
+the reference's statistical law tests, exact replay of the Generator
+consumption, and the spec32k workload."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle.sampler import verify_boundary_gap
+from pagellm_amd import workloads
+from pagellm_amd.speculative import verify, verify_batch
+
+pytestmark = pytest.mark.gpu
+
+
+def _dist(rng, V, sharp=1.0):
+    x = np.exp(rng.standard_normal(V) * sharp)
+    return x / x.sum()
+
+
+@pytest.mark.parametrize("k", [1, 2, 3])
+def test_kat_verify_law(kats, k):
+    c = kats["verify_law"]
+    rng = np.random.default_rng(k)
+    V = c["V"]
+    p = np.stack([_dist(rng, V, c["sharp"]) for _ in range(k + 1)])
+    q = np.stack([_dist(rng, V, c["sharp"]) for _ in range(k)])
+    trials = c["trials"] // 2
+    first = np.zeros(V)
+    joint = np.zeros((V, V))
+    n_joint = 0
+    for _ in range(trials):
+        xs = [oracle.draw(q[i], rng) for i in range(k)]
+        out, _ = verify(p, q, xs, rng)
+        first[out[0]] += 1
+        if len(out) >= 2:
+            joint[out[0], out[1]] += 1
+            n_joint += 1
+    assert 0.5 * np.abs(first / trials - p[0]).sum() < c["tv_first"]
+    if k >= 2:
+        assert 0.5 * np.abs(joint.sum(0) / n_joint - p[1]).sum() < c["tv_conditional"]
+
+
+def test_kat_verify_identical(kats):
+    c = kats["verify_identical"]
+    rng = np.random.default_rng(c["rng_seed"])
+    p = np.stack([_dist(rng, c["V"]) for _ in range(c["rows"])])
+    for _ in range(c["trials"]):
+        xs = [oracle.draw(p[i], rng) for i in range(c["k"])]
+        out, acc = verify(p, p[: c["k"]], xs, rng)
+        assert acc == c["k"] and out[: c["k"]] == xs and len(out) == c["k"] + 1
+
+
+def test_verify_replays_generator_exactly():
+    """Same outputs as the oracle fed by an identical Generator, and both
+    Generators end in the same state (same number of draws)."""
+    g = np.random.default_rng(11)
+    for trial in range(300):
+        V = int(g.integers(2, 50))
+        k = int(g.integers(0, 6))
+        p = np.stack([_dist(g, V, 1.5) for _ in range(k + 1)])
+        q = np.stack([_dist(g, V, 1.5) for _ in range(k)]) if k else np.zeros((0, V))
+        draft = [int(g.integers(0, V)) for _ in range(k)]
+        a, b = np.random.default_rng([5, trial]), np.random.default_rng([5, trial])
+        got = verify(p, q, draft, a)
+        ref = oracle.verify(p, q, draft, b)
+        assert got == ref, trial
+        assert a.random() == b.random()
+
+
+def test_spec32k_parity():
+    w = workloads.spec32k()
+    toks, n = verify_batch(w["p"], w["q"], w["draft"], w["accept_u"], w["resample_u"])
+    rt, rn = oracle.verify_batch(w["p"], w["q"], w["draft"], w["accept_u"], w["resample_u"])
+    boundary = 0
+    for b in range(len(n)):
+        if n[b] != rn[b] or not np.array_equal(toks[b], rt[b]):
+            gap = verify_boundary_gap(w["p"][b], w["q"][b], list(w["draft"][b]), w["accept_u"][b], w["resample_u"][b])
+            assert gap < 1e-6, (b, gap)
+            boundary += 1
+    print(f"spec32k rows {len(n)}, accepted mean {n.mean():.3f}, boundary cases {boundary}")
+
+
+def test_spec32k_float32_inputs():
+    w = workloads.spec32k(rows=8)
+    p32, q32 = w["p"].astype(np.float32), w["q"].astype(np.float32)
+    toks, n = verify_batch(p32, q32, w["draft"], w["accept_u"], w["resample_u"])
+    rt, rn = oracle.verify_batch(p32.astype(np.float64), q32.astype(np.float64), w["draft"], w["accept_u"],
+                                 w["resample_u"])
+    assert np.array_equal(n, rn) and np.array_equal(toks, rt)
+
+
+def test_verify_edge_cases():
+    p = np.array([[0.5, 0.5], [0.1, 0.9], [0.2, 0.8]])
+    q = np.array([[0.25, 0.75], [0.5, 0.5]])
+    # k = 0: a single draw from p[0]
+    toks, n = verify_batch(p[None, :1], np.zeros((1, 0, 2)), np.zeros((1, 0), np.int64), np.zeros((1, 0)), [0.7])
+    assert list(toks[0]) == [1] and n[0] == 0
+    # zero residual: p <= q everywhere at the rejected position -> draw from p
+    toks, n = verify_batch(np.array([[[0.1, 0.0], [0.5, 0.5]]]), np.array([[[0.2, 0.5]]]), [[0]], [[0.6]], [0.99])
+    assert list(toks[0]) == [0, -1] and n[0] == 0
+    # strict '<': u equal to the ratio rejects
+    toks, n = verify_batch(np.array([[[0.5, 0.5], [1.0, 0.0]]]), np.array([[[1.0, 0.0]]]), [[0]], [[0.5]], [0.0])
+    assert n[0] == 0
+    with pytest.raises(IndexError):
+        verify_batch(p[None], q[None], [[0, 2]], [[0.1, 0.1]], [0.5])
