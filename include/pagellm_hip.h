@@ -44,8 +44,6 @@ extern "C" {
 /* plh_sample flags */
 #define PLH_SAMPLE_ROWWISE 1 /* one workgroup per row (the general kernel) */
 
-/* plh_set_option options */
-#define PLH_OPT_TOPP_CAP 1 /* candidates kept per 8192-token chunk for top-p rows, 16..8192 (default 640) */
 
 typedef struct plh_ctx plh_ctx;
 

@@ -25,7 +25,6 @@ PLH_ERR_NO_DEVICE = -5
 PLH_F32 = 0
 PLH_F64 = 1
 PLH_SAMPLE_ROWWISE = 1
-PLH_OPT_TOPP_CAP = 1
 
 _c_int, _c_i64, _c_sz, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
 
@@ -207,9 +206,6 @@ class Context:
 
     def set_stream(self, stream_handle: int | None) -> None:
         self._check(self.lib.plh_set_stream(self.handle, stream_handle or None))
-
-    def set_topp_cap(self, cap: int) -> None:
-        self._check(self.lib.plh_set_option(self.handle, PLH_OPT_TOPP_CAP, int(cap)))
 
     def fallback_rows(self) -> int:
         v = _c_i64()

@@ -6,27 +6,20 @@
 #include <new>
 #include <string>
 
-#include "../../include/pagellm_hip.h"
+#include "pagellm_hip.h"
 #include "plh_kernels.h"
 
 struct plh_ctx {
   int device = 0;
   hipStream_t own_stream = nullptr;
   hipStream_t stream = nullptr;
-  // split-kernel workspace
-  void* ws = nullptr;
-  size_t ws_bytes = 0;
-  uint32_t* row_count = nullptr;  // separate: must stay zero between launches
-  size_t row_count_n = 0;
   unsigned long long* fallback = nullptr;
-  int topp_cap = 640;
   std::string err;
 };
 
 namespace {
 
 constexpr int kMaxVBitmap = 262144;
-constexpr int kMaxSplitChunks = 256;
 
 int fail(plh_ctx* c, int code, const char* fmt, const char* detail = nullptr) {
   if (c != nullptr) {
@@ -57,46 +50,6 @@ int use_device(plh_ctx* c) {
 }
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
-
-int ensure_workspace(plh_ctx* c, int B, int G, int cap, plh::SampleArgs& a) {
-  const size_t nchunks = (size_t)B * G;
-  const size_t sums = align_up(nchunks * sizeof(plh::ChunkSum), 256);
-  const size_t ncand = nchunks * (size_t)cap;
-  const size_t cz = align_up(ncand * sizeof(double), 256);
-  const size_t cidx = align_up(ncand * sizeof(int32_t), 256);
-  const size_t cp = cz;
-  const size_t need = sums + cz + cidx + cp;
-  if (need > c->ws_bytes) {
-    if (c->ws != nullptr) {
-      PLH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-      PLH_HIP(c, hipFree(c->ws), "hipFree");
-      c->ws = nullptr;
-      c->ws_bytes = 0;
-    }
-    PLH_HIP(c, hipMalloc(&c->ws, need), "hipMalloc(workspace)");
-    c->ws_bytes = need;
-  }
-  if ((size_t)B > c->row_count_n) {
-    if (c->row_count != nullptr) {
-      PLH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
-      PLH_HIP(c, hipFree(c->row_count), "hipFree");
-      c->row_count = nullptr;
-      c->row_count_n = 0;
-    }
-    const size_t n = B < 1024 ? 1024 : (size_t)B;
-    PLH_HIP(c, hipMalloc(&c->row_count, n * sizeof(uint32_t)), "hipMalloc(row counters)");
-    PLH_HIP(c, hipMemsetAsync(c->row_count, 0, n * sizeof(uint32_t), c->stream), "hipMemsetAsync");
-    c->row_count_n = n;
-  }
-  char* base = static_cast<char*>(c->ws);
-  a.sums = reinterpret_cast<plh::ChunkSum*>(base);
-  a.cz = reinterpret_cast<double*>(base + sums);
-  a.cidx = reinterpret_cast<int32_t*>(base + sums + cz);
-  a.cp = reinterpret_cast<double*>(base + sums + cz + cidx);
-  a.row_count = c->row_count;
-  a.fallback_rows = c->fallback;
-  return PLH_OK;
-}
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -135,8 +88,6 @@ void plh_destroy(plh_ctx* c) {
   if (c == nullptr) return;
   (void)hipSetDevice(c->device);
   if (c->stream != nullptr) (void)hipStreamSynchronize(c->stream);
-  if (c->ws != nullptr) (void)hipFree(c->ws);
-  if (c->row_count != nullptr) (void)hipFree(c->row_count);
   if (c->fallback != nullptr) (void)hipFree(c->fallback);
   if (c->own_stream != nullptr) (void)hipStreamDestroy(c->own_stream);
   delete c;
@@ -152,11 +103,8 @@ int plh_set_stream(plh_ctx* c, void* stream) {
 
 int plh_set_option(plh_ctx* c, int option, int64_t value) {
   if (c == nullptr) return PLH_ERR_INVALID_ARG;
+  (void)value;
   switch (option) {
-    case PLH_OPT_TOPP_CAP:
-      if (value < 16 || value > plh::kChunk) return fail(c, PLH_ERR_INVALID_ARG, "PLH_OPT_TOPP_CAP must be in [16, 8192]%s");
-      c->topp_cap = (int)value;
-      return PLH_OK;
     default:
       return fail(c, PLH_ERR_INVALID_ARG, "unknown option%s");
   }
@@ -254,18 +202,11 @@ int plh_sample(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, int
   a.uniforms = uniforms;
   a.out_ids = out_ids;
   a.out_probs = out_probs;
-  const int G = (V + plh::kChunk - 1) / plh::kChunk;
-  hipError_t e;
-  if (out_probs != nullptr || (flags & PLH_SAMPLE_ROWWISE) || G > kMaxSplitChunks) {
-    e = plh::launch_sample_rows(a, dtype == PLH_F64, vec, c->stream);
-  } else {
-    a.G = G;
-    a.cap = c->topp_cap;
-    a.xcd_map = B >= 8 ? 1 : 0;
-    rc = ensure_workspace(c, B, G, a.cap, a);
-    if (rc != PLH_OK) return rc;
-    e = plh::launch_sample_split(a, dtype == PLH_F64, vec, c->stream);
-  }
+  a.fallback_rows = c->fallback;
+  // the single-pass kernel keeps per-row state in LDS sized for V <= 262144
+  const hipError_t e = (out_probs != nullptr || (flags & PLH_SAMPLE_ROWWISE) || V > kMaxVBitmap)
+                           ? plh::launch_sample_rows(a, dtype == PLH_F64, vec, c->stream)
+                           : plh::launch_sample_fast(a, dtype == PLH_F64, vec, c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "plh_sample launch");
   return PLH_OK;
 }

@@ -1,0 +1,154 @@
+// Building blocks of the single-pass row kernel: a table-driven float64
+// exp, value-range histograms for selection, and a bitonic sort of small
+// LDS lists.
+#pragma once
+
+#include <limits.h>
+
+#include "plh_device.h"
+
+namespace plh {
+
+// ------------------------------------------------------------------- exp
+// exp(d) for d <= 0 in float64, <= 2 ulp: d = k*ln2/64 + r with a two-part
+// ln2/64 (Cody-Waite reduction), exp(r) by its degree-5 Taylor polynomial
+// (|r| <= ln2/128, truncation < 4e-17), times 2^(k/64) from a 64-entry
+// table of 2^(j/64) built on the device, scaled by 2^(k>>6) with ldexp.
+// The split of ln2 is the classic fdlibm one (a 32-bit head, exact k*head
+// for |k| < 2^21).
+constexpr double kLn2Hi = 6.93147180369123816490e-01;
+constexpr double kLn2Lo = 1.90821492927058770002e-10;
+
+__device__ __forceinline__ void init_exp_table(double* tab) {
+  if (threadIdx.x < 64) tab[threadIdx.x] = exp2((double)threadIdx.x / 64.0);
+}
+
+__device__ __forceinline__ double fast_exp_neg(double d, const double* tab) {
+  if (!(d > -745.2)) return 0.0;  // also -inf
+  const double kd = __builtin_rint(d * (64.0 / 0.6931471805599453));
+  const int k = (int)kd;
+  double r = fma(-kd, kLn2Hi / 64.0, d);
+  r = fma(-kd, kLn2Lo / 64.0, r);
+  double q = fma(r, 1.0 / 120.0, 1.0 / 24.0);
+  q = fma(q, r, 1.0 / 6.0);
+  q = fma(q, r, 0.5);
+  q = fma(q, r, 1.0);
+  q = fma(q, r, 1.0);
+  return ldexp(tab[k & 63] * q, k >> 6);
+}
+
+// ------------------------------------------------------- value histograms
+// bin(v) = floor((v - lo) * scale) clamped to [0, nb-1]: monotone
+// non-decreasing in v, so "bin(v) >= d" is a threshold rule on v.
+struct Affine {
+  double lo, scale;
+  int nb;
+  __device__ __forceinline__ int bin(double v) const {
+    if (!(v > lo)) return 0;  // v <= lo (and -inf)
+    const double t = (v - lo) * scale;
+    return t >= (double)(nb - 1) ? nb - 1 : (int)t;
+  }
+};
+
+__device__ __forceinline__ Affine make_affine(double lo, double hi, int nb) {
+  Affine a;
+  a.nb = nb;
+  a.lo = lo;
+  a.scale = (hi > lo && hi - lo < INFINITY) ? (double)(nb - 1) / (hi - lo) : 0.0;
+  if (!(a.scale < INFINITY)) a.scale = 0.0;
+  return a;
+}
+
+// ------------------------------------------------------------ LDS sort
+// Bitonic sort of n <= N_max entries (key, idx, w) in LDS, into the order
+// where `before(ka, ia, kb, ib)` holds for earlier entries.  Entries past n
+// are padded with (pad_key, INT_MAX) which must sort last.
+template <class Before>
+__device__ __forceinline__ void lds_bitonic(uint64_t* key, int* idx, uint64_t* w, int n, uint64_t pad_key,
+                                            const Before& before) {
+  int N = 2;
+  while (N < n) N <<= 1;
+  for (int i = threadIdx.x; i < N; i += kThreads)
+    if (i >= n) {
+      key[i] = pad_key;
+      idx[i] = INT_MAX;
+      w[i] = 0ull;
+    }
+  __syncthreads();
+  for (int k = 2; k <= N; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < N; i += kThreads) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const uint64_t ka = key[i], kb = key[ixj];
+          const int ia = idx[i], ib = idx[ixj];
+          const bool sw = ((i & k) == 0) ? before(kb, ib, ka, ia) : before(ka, ia, kb, ib);
+          if (sw) {
+            key[i] = kb;
+            key[ixj] = ka;
+            idx[i] = ib;
+            idx[ixj] = ia;
+            const uint64_t t = w[i];
+            w[i] = w[ixj];
+            w[ixj] = t;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Descending walk over nb histogram bins (counts and/or masses in LDS):
+// the bin where the running total (from `above`) first reaches target.
+struct Pick {
+  bool found;
+  int d;
+  uint64_t above;
+};
+
+template <bool MASS>
+__device__ __forceinline__ Pick pick_desc(const uint32_t* cnt, const uint64_t* mass, int nb, uint64_t above,
+                                          uint64_t target, uint64_t* redu, int* ctl, uint64_t* ctlu) {
+  const int per = (nb + kThreads - 1) / kThreads;  // nb <= 2 * kThreads
+  uint64_t v[2];
+  uint64_t s = 0;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    v[j] = 0;
+    const int r = (int)threadIdx.x * per + j;
+    if (j < per && r < nb) {
+      const int d = nb - 1 - r;
+      v[j] = MASS ? mass[d] : (uint64_t)cnt[d];
+    }
+    s += v[j];
+  }
+  uint64_t tot;
+  const uint64_t ex = block_excl_scan<uint64_t>(s, redu, &tot);
+  if (above + tot < target) return Pick{false, -1, above + tot};
+  if (threadIdx.x == 0) ctl[0] = INT_MAX;
+  __syncthreads();
+  uint64_t run = above + ex, myrun = 0;
+  int myrank = INT_MAX;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = (int)threadIdx.x * per + j;
+    if (j < per && r < nb && myrank == INT_MAX) {
+      if (run + v[j] >= target) {
+        myrank = r;
+        myrun = run;
+      }
+      run += v[j];
+    }
+  }
+  if (myrank != INT_MAX) lds_min(&ctl[0], myrank);
+  __syncthreads();
+  const int rk = ctl[0];
+  if (myrank == rk) ctlu[1] = myrun;
+  __syncthreads();
+  const Pick p{true, nb - 1 - rk, ctlu[1]};
+  __syncthreads();
+  return p;
+}
+
+}  // namespace plh

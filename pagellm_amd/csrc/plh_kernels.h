@@ -7,19 +7,6 @@
 
 namespace plh {
 
-constexpr int kChunkTiles = 4;                 // 2048-element tiles per chunk
-constexpr int kChunk = kChunkTiles * 2048;     // elements per chunk workgroup (16 per thread)
-
-// Per-(row, chunk) summary written by the split kernel's chunk pass.
-struct ChunkSum {
-  double zmax;   // largest penalised logit in the chunk
-  int argmax;    // its lowest index (vocabulary index)
-  int ncand;     // candidates retained (-1: more than the capacity)
-  double s;      // sum over the chunk of exp(y - zmax/T)  (top-p rows)
-  double umax;   // largest penalised logit NOT retained (-inf: none)
-  uint64_t tile[kChunkTiles];  // temperature-only rows: fixed-point mass per tile
-};
-
 struct SampleArgs {
   const void* logits;
   int64_t ld;
@@ -33,14 +20,7 @@ struct SampleArgs {
   const double* uniforms;
   int32_t* out_ids;
   double* out_probs;
-  // split-kernel workspace
-  uint32_t* row_count;  // B arrival counters, zero between launches
-  ChunkSum* sums;       // B * G
-  double* cz;           // B * G * cap
-  int32_t* cidx;
-  double* cp;
-  unsigned long long* fallback_rows;
-  int G, cap, xcd_map;
+  unsigned long long* fallback_rows;  // rows finished by the general path
 };
 
 struct DrawArgs {
@@ -75,7 +55,7 @@ struct VerifyArgs {
 };
 
 hipError_t launch_sample_rows(const SampleArgs& a, bool f64, bool vec, hipStream_t s);
-hipError_t launch_sample_split(const SampleArgs& a, bool f64, bool vec, hipStream_t s);
+hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, hipStream_t s);
 hipError_t launch_draw(const DrawArgs& a, bool f64, hipStream_t s);
 hipError_t launch_penalize(const PenalizeArgs& a, bool f64, hipStream_t s);
 hipError_t launch_verify(const VerifyArgs& a, bool f64, hipStream_t s);

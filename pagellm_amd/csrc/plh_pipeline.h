@@ -2,11 +2,9 @@
 //
 // The pipeline restates src/pagellm/engine/sampling.py:65-107 (penalty ->
 // temperature -> top-k -> softmax -> top-p -> inverse-CDF draw, greedy
-// argmax) over an abstract element source:
-//   * RowSource streams a whole logits row from HBM (general path, and the
-//     path that can export the processed distribution);
-//   * CandSource walks the candidates that the chunk pass of the split
-//     kernel retained for a row (index order, chunk by chunk).
+// argmax) over an element source; RowSource streams a whole logits row from
+// HBM once per pass.  It is the general path (any parameters, any
+// distribution) and the path that exports the processed distribution.
 // Sorting is replaced by selection: top-k is an MSD radix select by count on
 // order-preserving 64-bit keys of the penalised logits; the top-p cut is an
 // MSD radix select by fixed-point probability mass on the bits of p, in the
@@ -23,7 +21,6 @@ namespace plh {
 constexpr int kBins = 2048;  // widest radix digit is 11 bits
 constexpr int kSmall = 512;  // a bin this small is finished by an LDS sort
 constexpr int kMaxVBitmap = 262144;  // penalty bitmap capacity (vocabulary size)
-constexpr int kMaxChunks = 256;
 
 struct Smem {
   double redd[kWaves];
@@ -38,7 +35,6 @@ struct Smem {
   uint64_t lkey[kSmall];
   uint64_t lw[kSmall];
   int32_t lidx[kSmall];
-  int cpref[kMaxChunks + 1];
   uint32_t bitmap[kMaxVBitmap / 32];
 };
 
@@ -132,72 +128,6 @@ struct RowSource {
     load4(base, z, idx, valid, addr);
 #pragma unroll
     for (int l = 0; l < 4; ++l) p[l] = valid[l] ? p_of(pc, z[l]) : 0.0;
-  }
-};
-
-// The candidates retained for one row: chunk g holds cnt_g entries at
-// [g*cap, g*cap + cnt_g) of cz/cidx (and cp once prepared); sm.cpref holds
-// the running counts.  Flattened position order is vocabulary order.
-struct CandSource {
-  const double* cz;
-  const int32_t* cidx;
-  double* cp;
-  const int* pref;  // LDS, G + 1 entries
-  int G, cap, total;
-  bool prepared;
-
-  __device__ __forceinline__ int n() const { return total; }
-
-  __device__ __forceinline__ int find_chunk(int p) const {
-    int lo = 0, hi = G;  // pref[lo] <= p < pref[hi]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (pref[mid] <= p) lo = mid; else hi = mid;
-    }
-    return lo;
-  }
-
-  __device__ __forceinline__ void load4(int base, double z[4], int idx[4], bool valid[4], int addr[4]) const {
-    const int p0 = base + 4 * (int)threadIdx.x;
-    int g = p0 < total ? find_chunk(p0) : 0;
-#pragma unroll
-    for (int l = 0; l < 4; ++l) {
-      const int p = p0 + l;
-      valid[l] = p < total;
-      if (valid[l]) {
-        while (p >= pref[g + 1]) ++g;
-        const int a = g * cap + (p - pref[g]);
-        addr[l] = a;
-        z[l] = cz[a];
-        idx[l] = cidx[a];
-      } else {
-        addr[l] = 0;
-        z[l] = -INFINITY;
-        idx[l] = INT_MAX;
-      }
-    }
-  }
-
-  __device__ __forceinline__ void prepare_p(const PCalc& pc, Smem&) {
-    for (int base = 0; base < total; base += 4 * kThreads) {
-      double z[4];
-      int idx[4], addr[4];
-      bool valid[4];
-      load4(base, z, idx, valid, addr);
-#pragma unroll
-      for (int l = 0; l < 4; ++l)
-        if (valid[l]) cp[addr[l]] = p_of(pc, z[l]);
-    }
-    __syncthreads();
-    prepared = true;
-  }
-
-  __device__ __forceinline__ void load4p(int base, double z[4], int idx[4], bool valid[4], double p[4],
-                                         const PCalc& pc) const {
-    int addr[4];
-    load4(base, z, idx, valid, addr);
-#pragma unroll
-    for (int l = 0; l < 4; ++l) p[l] = valid[l] ? (prepared ? cp[addr[l]] : p_of(pc, z[l])) : 0.0;
   }
 };
 
