@@ -44,6 +44,10 @@ extern "C" {
 /* plh_sample flags */
 #define PLH_SAMPLE_ROWWISE 1 /* one workgroup per row (the general kernel) */
 
+/* plh_set_option options */
+#define PLH_OPT_KERNEL_TIMING 1 /* value 1: bracket the fast path's kernels with
+                                   HIP events (read by plh_kernel_times) */
+
 
 typedef struct plh_ctx plh_ctx;
 
@@ -59,9 +63,14 @@ const char* plh_last_error(const plh_ctx* ctx);
  * restores the context's own stream. */
 int plh_set_stream(plh_ctx* ctx, void* stream);
 int plh_set_option(plh_ctx* ctx, int option, int64_t value);
-/* Rows finished by the general row-wise pipeline inside the fast kernel,
- * cumulative since plh_create (waits for queued work). */
+/* Rows the fast path's merge kernel finished with the general row-wise
+ * pipeline, cumulative since plh_create (waits for queued work). */
 int plh_fallback_rows(plh_ctx* ctx, int64_t* out);
+/* While PLH_OPT_KERNEL_TIMING is on: device time of the fast path's
+ * streaming kernel and merge kernel summed over the plh_sample calls made
+ * since the last read, and their count.  Waits for those calls, then
+ * resets.  No reference counterpart (measurement only). */
+int plh_kernel_times(plh_ctx* ctx, double* stream_ms, double* merge_ms, int64_t* calls);
 
 /* Device memory helpers so numpy callers need no other GPU library.
  * plh_h2d / plh_d2h return once the copy is complete. */

@@ -25,6 +25,7 @@ PLH_ERR_NO_DEVICE = -5
 PLH_F32 = 0
 PLH_F64 = 1
 PLH_SAMPLE_ROWWISE = 1
+PLH_OPT_KERNEL_TIMING = 1
 
 _c_int, _c_i64, _c_sz, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
 
@@ -37,6 +38,8 @@ SIGNATURES = {
     "plh_set_stream": (_c_int, [_vp, _vp]),
     "plh_set_option": (_c_int, [_vp, _c_int, _c_i64]),
     "plh_fallback_rows": (_c_int, [_vp, ctypes.POINTER(_c_i64)]),
+    "plh_kernel_times": (_c_int, [_vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+                                  ctypes.POINTER(_c_i64)]),
     "plh_alloc": (_c_int, [_vp, ctypes.POINTER(_vp), _c_sz]),
     "plh_free": (_c_int, [_vp, _vp]),
     "plh_h2d": (_c_int, [_vp, _vp, _vp, _c_sz]),
@@ -211,6 +214,16 @@ class Context:
         v = _c_i64()
         self._check(self.lib.plh_fallback_rows(self.handle, ctypes.byref(v)))
         return int(v.value)
+
+    def set_kernel_timing(self, on: bool) -> None:
+        self._check(self.lib.plh_set_option(self.handle, PLH_OPT_KERNEL_TIMING, 1 if on else 0))
+
+    def kernel_times(self) -> tuple[float, float, int]:
+        """(streaming-kernel ms, merge-kernel ms, calls) summed over the fast-path
+        calls made since the last read while kernel timing was on."""
+        a, b, n = ctypes.c_double(), ctypes.c_double(), _c_i64()
+        self._check(self.lib.plh_kernel_times(self.handle, ctypes.byref(a), ctypes.byref(b), ctypes.byref(n)))
+        return float(a.value), float(b.value), int(n.value)
 
     # ------------------------------------------------------------- kernels
     def sample(self, logits_ptr, dtype_code, ld, B, V, hist_ids, hist_off, temperature, top_k, top_p,

@@ -3,8 +3,10 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <array>
 #include <new>
 #include <string>
+#include <vector>
 
 #include "pagellm_hip.h"
 #include "plh_kernels.h"
@@ -14,6 +16,16 @@ struct plh_ctx {
   hipStream_t own_stream = nullptr;
   hipStream_t stream = nullptr;
   unsigned long long* fallback = nullptr;
+  // fast-path workspace, reused by every call on this context; ws_done marks
+  // the end of the last call that used it (on ws_stream)
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  hipEvent_t ws_done = nullptr;
+  hipStream_t ws_stream = nullptr;
+  // PLH_OPT_KERNEL_TIMING: event triples (start, between, end) per timed call
+  bool timing = false;
+  std::vector<hipEvent_t> ev_free;
+  std::vector<std::array<hipEvent_t, 3>> ev_pending;
   std::string err;
 };
 
@@ -51,6 +63,27 @@ int use_device(plh_ctx* c) {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Makes the context's workspace at least `bytes` large and orders the
+// current stream after the last call that used it (possibly on another
+// stream).  Growing waits for that call and reallocates.
+int reserve_ws(plh_ctx* c, size_t bytes) {
+  if (bytes > c->ws_bytes) {
+    if (c->ws_stream != nullptr) PLH_HIP(c, hipStreamSynchronize(c->ws_stream), "hipStreamSynchronize");
+    if (c->ws != nullptr) {
+      PLH_HIP(c, hipFree(c->ws), "hipFree");
+      c->ws = nullptr;
+      c->ws_bytes = 0;
+    }
+    const size_t sz = align_up(bytes + bytes / 4, 1u << 20);
+    PLH_HIP(c, hipMalloc(&c->ws, sz), "hipMalloc(workspace)");
+    c->ws_bytes = sz;
+    c->ws_stream = nullptr;
+  }
+  if (c->ws_stream != nullptr && c->ws_stream != c->stream)
+    PLH_HIP(c, hipStreamWaitEvent(c->stream, c->ws_done, 0), "hipStreamWaitEvent");
+  return PLH_OK;
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -75,6 +108,7 @@ int plh_create(plh_ctx** out, int device) {
     c->stream = c->own_stream;
     if (hipMalloc(&c->fallback, sizeof(unsigned long long)) != hipSuccess) { rc = PLH_ERR_OUT_OF_MEMORY; break; }
     if (hipMemset(c->fallback, 0, sizeof(unsigned long long)) != hipSuccess) { rc = PLH_ERR_HIP; break; }
+    if (hipEventCreateWithFlags(&c->ws_done, hipEventDisableTiming) != hipSuccess) { rc = PLH_ERR_HIP; break; }
   } while (0);
   if (rc != PLH_OK) {
     plh_destroy(c);
@@ -88,6 +122,12 @@ void plh_destroy(plh_ctx* c) {
   if (c == nullptr) return;
   (void)hipSetDevice(c->device);
   if (c->stream != nullptr) (void)hipStreamSynchronize(c->stream);
+  if (c->ws_stream != nullptr) (void)hipStreamSynchronize(c->ws_stream);
+  if (c->ws != nullptr) (void)hipFree(c->ws);
+  if (c->ws_done != nullptr) (void)hipEventDestroy(c->ws_done);
+  for (auto& t : c->ev_pending)
+    for (hipEvent_t e : t) c->ev_free.push_back(e);
+  for (hipEvent_t e : c->ev_free) (void)hipEventDestroy(e);
   if (c->fallback != nullptr) (void)hipFree(c->fallback);
   if (c->own_stream != nullptr) (void)hipStreamDestroy(c->own_stream);
   delete c;
@@ -103,11 +143,38 @@ int plh_set_stream(plh_ctx* c, void* stream) {
 
 int plh_set_option(plh_ctx* c, int option, int64_t value) {
   if (c == nullptr) return PLH_ERR_INVALID_ARG;
-  (void)value;
   switch (option) {
+    case PLH_OPT_KERNEL_TIMING:
+      if (value != 0 && value != 1) return fail(c, PLH_ERR_INVALID_ARG, "PLH_OPT_KERNEL_TIMING takes 0 or 1%s");
+      c->timing = value != 0;
+      return PLH_OK;
     default:
       return fail(c, PLH_ERR_INVALID_ARG, "unknown option%s");
   }
+}
+
+int plh_kernel_times(plh_ctx* c, double* stream_ms, double* merge_ms, int64_t* calls) {
+  if (c == nullptr || stream_ms == nullptr || merge_ms == nullptr || calls == nullptr) return PLH_ERR_INVALID_ARG;
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  double a = 0.0, b = 0.0;
+  int64_t n = 0;
+  for (auto& t : c->ev_pending) {
+    PLH_HIP(c, hipEventSynchronize(t[2]), "hipEventSynchronize");
+    float x = 0.f, y = 0.f;
+    PLH_HIP(c, hipEventElapsedTime(&x, t[0], t[1]), "hipEventElapsedTime");
+    PLH_HIP(c, hipEventElapsedTime(&y, t[1], t[2]), "hipEventElapsedTime");
+    a += x;
+    b += y;
+    ++n;
+  }
+  for (auto& t : c->ev_pending)
+    for (hipEvent_t e : t) c->ev_free.push_back(e);
+  c->ev_pending.clear();
+  *stream_ms = a;
+  *merge_ms = b;
+  *calls = n;
+  return PLH_OK;
 }
 
 int plh_fallback_rows(plh_ctx* c, int64_t* out) {
@@ -203,11 +270,35 @@ int plh_sample(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, int
   a.out_ids = out_ids;
   a.out_probs = out_probs;
   a.fallback_rows = c->fallback;
-  // the single-pass kernel keeps per-row state in LDS sized for V <= 262144
-  const hipError_t e = (out_probs != nullptr || (flags & PLH_SAMPLE_ROWWISE) || V > kMaxVBitmap)
-                           ? plh::launch_sample_rows(a, dtype == PLH_F64, vec, c->stream)
-                           : plh::launch_sample_fast(a, dtype == PLH_F64, vec, c->stream);
+  const bool f64 = dtype == PLH_F64;
+  // the fast path gathers per-row state in LDS sized for V <= 262144
+  if (out_probs != nullptr || (flags & PLH_SAMPLE_ROWWISE) || V > kMaxVBitmap) {
+    const hipError_t e = plh::launch_sample_rows(a, f64, vec, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "plh_sample launch");
+    return PLH_OK;
+  }
+  rc = reserve_ws(c, plh::fast_ws_bytes(B, V, f64));
+  if (rc != PLH_OK) return rc;
+  a.ws = plh::fast_ws_layout(c->ws, B, V, f64);
+  std::array<hipEvent_t, 3> ev{};
+  if (c->timing) {
+    for (auto& e : ev) {
+      if (c->ev_free.empty()) {
+        hipEvent_t n = nullptr;
+        PLH_HIP(c, hipEventCreate(&n), "hipEventCreate");
+        c->ev_free.push_back(n);
+      }
+      e = c->ev_free.back();
+      c->ev_free.pop_back();
+    }
+    c->ev_pending.push_back(ev);
+    PLH_HIP(c, hipEventRecord(ev[0], c->stream), "hipEventRecord");
+  }
+  const hipError_t e = plh::launch_sample_fast(a, f64, vec, c->stream, ev[1]);
   if (e != hipSuccess) return hip_fail(c, e, "plh_sample launch");
+  if (c->timing) PLH_HIP(c, hipEventRecord(ev[2], c->stream), "hipEventRecord");
+  PLH_HIP(c, hipEventRecord(c->ws_done, c->stream), "hipEventRecord");
+  c->ws_stream = c->stream;
   return PLH_OK;
 }
 

@@ -46,7 +46,8 @@ struct Affine {
   __device__ __forceinline__ int bin(double v) const {
     if (!(v > lo)) return 0;  // v <= lo (and -inf)
     const double t = (v - lo) * scale;
-    return t >= (double)(nb - 1) ? nb - 1 : (int)t;
+    if (t >= (double)(nb - 1)) return nb - 1;
+    return t > 0.0 ? (int)t : 0;  // also NaN (+inf times a zero scale)
   }
 };
 

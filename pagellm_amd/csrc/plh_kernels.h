@@ -7,6 +7,26 @@
 
 namespace plh {
 
+// Per-chunk partial left by k_sample_chunks for k_sample_final.
+struct ChunkPart {
+  double zmax;   // largest finite penalised logit of the chunk (-inf if none)
+  double umax;   // largest finite one not kept as a candidate (-inf if none)
+  double best_z; // greedy rows: the chunk's argmax value ...
+  int best_idx;  // ... and its token id
+  int n;         // candidates written (at most capc)
+};
+
+// Workspace of the two-launch fast path, carved from one device buffer.
+struct ChunkWs {
+  ChunkPart* part;  // [B * C]
+  double* seg_m;    // [B * C * 8] per-wave segment max of z / T
+  double* seg_s;    // [B * C * 8] per-wave segment sum of exp(z / T - max)
+  double* cz;       // [B * C * capc] candidate penalised logits
+  int32_t* ci;      // [B * C * capc] candidate token ids
+  int C;            // chunks per row
+  int capc;         // candidate slots per chunk
+};
+
 struct SampleArgs {
   const void* logits;
   int64_t ld;
@@ -21,6 +41,7 @@ struct SampleArgs {
   int32_t* out_ids;
   double* out_probs;
   unsigned long long* fallback_rows;  // rows finished by the general path
+  ChunkWs ws;                         // fast path only
 };
 
 struct DrawArgs {
@@ -55,7 +76,13 @@ struct VerifyArgs {
 };
 
 hipError_t launch_sample_rows(const SampleArgs& a, bool f64, bool vec, hipStream_t s);
-hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, hipStream_t s);
+// Fast path: workspace bytes for a [B, V] batch, its layout inside `base`
+// (256-byte aligned), and the two launches.
+size_t fast_ws_bytes(int B, int V, bool f64);
+ChunkWs fast_ws_layout(void* base, int B, int V, bool f64);
+// `between`, when not null, is recorded on s between the two kernels.
+hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, hipStream_t s,
+                              hipEvent_t between = nullptr);
 hipError_t launch_draw(const DrawArgs& a, bool f64, hipStream_t s);
 hipError_t launch_penalize(const PenalizeArgs& a, bool f64, hipStream_t s);
 hipError_t launch_verify(const VerifyArgs& a, bool f64, hipStream_t s);

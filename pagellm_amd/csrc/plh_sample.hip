@@ -1,44 +1,60 @@
 // gfx950 kernels for the batched sampler (src/pagellm/engine/sampling.py:52-111).
 //
-//   k_sample_fast   one 512-thread workgroup per row, one pass over HBM.
-//                   The row streams through registers with 16-byte
-//                   non-temporal loads, one iteration (16384 tokens) ahead.
-//                   Per row mode:
-//                     greedy       argmax of the penalised logits;
-//                     temperature  per-wave segment softmax partials, then
-//                                  one 2048-token segment is rescanned for
-//                                  the inverse-CDF draw;
-//                     top-k        candidates >= a running lower bound of the
-//                                  k-th largest, kept in LDS;
-//                     top-p        segment partials for the normaliser plus
-//                                  the largest tokens (a projected count) in
-//                                  LDS.
-//                   Selection inside LDS uses value-range histograms and
-//                   small bitonic sorts; the draw is an exact fixed-point
-//                   search in vocabulary order.  A row the candidates cannot
-//                   decide exactly is finished by the general pipeline in
-//                   the same workgroup.
-//   k_sample_rows   the general pipeline for every row (and the only kernel
-//                   that exports the processed distribution, probs()).
-//   k_draw          inverse-CDF draw from given distributions (draw()).
-//   k_penalize      repetition penalty on a copy (apply_repetition_penalty()).
+// Fast path (V <= 262144, no probability export), two launches:
+//   k_sample_chunks  B x C workgroups of 512 threads.  Workgroup (row, c)
+//                    reads the c-th 64 KB chunk of the row once, with
+//                    16-byte non-temporal loads (32 fp32 or 16 fp64 tokens
+//                    per thread), penalises it in float64 registers and
+//                    leaves per-chunk partials in a workspace:
+//                      greedy       the chunk's argmax;
+//                      temperature  per-wave segment softmax partials
+//                                   (max, sum of exp);
+//                      top-k/top-p  the chunk's largest tokens (a value
+//                                   histogram picks the threshold) and the
+//                                   largest token left out; top-p-only rows
+//                                   also leave the segment partials.
+//                    Every chunk costs one 64 KB read whatever its row's
+//                    mode, and the hardware dispatcher spreads the B x C
+//                    workgroups over the CUs, so mixed batches stay
+//                    balanced.
+//   k_sample_final   one workgroup per row merges the partials: argmax;
+//                    normaliser and the segment holding the inverse-CDF
+//                    point (rescanned with the same arithmetic); or exact
+//                    selection over the gathered candidates (k-th largest,
+//                    top-p cut, fixed-point draw in vocabulary order).  A
+//                    row the candidates cannot decide exactly is finished
+//                    by the general pipeline in the same workgroup.
+// General path:
+//   k_sample_rows    the general pipeline for every row (and the only kernel
+//                    that exports the processed distribution, probs()).
+// Others:
+//   k_draw           inverse-CDF draw from given distributions (draw()).
+//   k_penalize       repetition penalty on a copy (apply_repetition_penalty()).
 #include "plh_fast.h"
 #include "plh_kernels.h"
 #include "plh_pipeline.h"
 
 namespace plh {
 
-constexpr int kU = 8;                              // 16-byte loads per thread per iteration
-constexpr int kE = 4 * kU;                         // tokens per thread per iteration
-constexpr int kSegLen = kE * kWave;                // 2048: one wave's contiguous share of an iteration
-constexpr int kIterLen = kSegLen * kWaves;         // 16384 tokens per iteration
-constexpr int kMaxSegs = kMaxVBitmap / kSegLen;    // 128
-constexpr int kHB = 1024;                          // histogram bins
-constexpr int kSortMax = 2048;                     // LDS sort list
-constexpr int kCandBytes = 80 * 1024;              // candidate store
+constexpr int kU = 8;             // 16-byte loads per thread per chunk
+constexpr int kHB = 1024;         // histogram bins
+constexpr int kSortMax = 2048;    // LDS sort list
+constexpr int kCandCap = 8192;    // candidates one row gathers in LDS
+constexpr int kCapChunk = 1024;   // candidate slots per chunk, at most
 constexpr int kSelLevels = 4;
 
-enum RowMode { kGreedy = 0, kTemp = 1, kTopK = 2, kTopP = 3 };
+// Chunk geometry per input type: a wave-wide 16-byte load covers kSpan
+// consecutive tokens, a wave owns one contiguous segment of kSeg tokens and
+// a workgroup one chunk of kChunk tokens (64 KB).
+template <typename TIn>
+struct Geo {
+  static constexpr int kVW = 16 / (int)sizeof(TIn);
+  static constexpr int kEpt = kU * kVW;
+  static constexpr int kSpan = kWave * kVW;
+  static constexpr int kSeg = kEpt * kWave;
+  static constexpr int kChunk = kSeg * kWaves;
+};
+constexpr int kSegMax = Geo<float>::kSeg;
 
 struct SortList {
   uint64_t key[kSortMax];
@@ -46,6 +62,7 @@ struct SortList {
   int idx[kSortMax];
 };
 
+// LDS of k_sample_final (about 150 KB: one workgroup per CU).
 struct FastSmem {
   double redd[kWaves];
   uint64_t redu[kWaves];
@@ -53,27 +70,21 @@ struct FastSmem {
   int ctl[8];
   uint64_t ctlu[4];
   double exp_tab[64];
-  double seg_m[kMaxSegs];
-  double seg_s[kMaxSegs];
+  int cnt_c[64];
   uint32_t hcnt[kHB];
   uint64_t hmass[kHB];
   union {
-    uint32_t bitmap[kMaxVBitmap / 32];  // while streaming
-    SortList sl;                        // while finishing
+    uint32_t segbits[kSegMax / 32];  // penalty bits of the rescanned segment
+    SortList sl;                     // selection and draw
   } u;
-  alignas(16) unsigned char cand[kCandBytes];
-  int cand_n;
+  double cz[kCandCap];
+  int ci[kCandCap];
 };
 
 union SmemAll {
   FastSmem f;
   Smem g;
 };
-
-template <typename TIn>
-constexpr int cand_cap() {
-  return kCandBytes / (int)(sizeof(TIn) + 4);
-}
 
 // Workgroup barrier ordering LDS only: global loads issued ahead of it stay
 // in flight.
@@ -120,270 +131,243 @@ __global__ __launch_bounds__(kThreads) void k_sample_rows(SampleArgs a) {
   if (threadIdx.x == 0) a.out_ids[row] = id;
 }
 
-// ------------------------------------------------------------- streaming
-
-typedef float f4_t __attribute__((ext_vector_type(4)));
-typedef double d2_t __attribute__((ext_vector_type(2)));
-
-template <typename TIn>
-struct RawIter;
-template <>
-struct RawIter<float> {
-  f4_t v[kU];
-};
-template <>
-struct RawIter<double> {
-  d2_t v[2 * kU];
-};
-
-// Token (j, s) of the calling lane in the iteration starting at `base`:
-// base + wave*2048 + j*256 + 4*lane + s.  Each load instruction of a wave
-// covers 1 KB of contiguous HBM.
-__device__ __forceinline__ int lane_off(int base) { return base + wave() * kSegLen + 4 * lane(); }
-
-template <bool VEC>
-__device__ __forceinline__ void load_iter(const float* x, int V, int base, RawIter<float>& r) {
-  const int off = lane_off(base);
-  const bool full = VEC && base + kIterLen <= V;  // uniform: no bounds checks needed
-#pragma unroll
-  for (int j = 0; j < kU; ++j) {
-    const int p = off + j * 256;
-    if (full || (VEC && p + 3 < V)) {
-      r.v[j] = __builtin_nontemporal_load(reinterpret_cast<const f4_t*>(x + p));
-    } else {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) r.v[j][s] = (p + s < V) ? x[p + s] : -INFINITY;
-    }
-  }
-}
-
-template <bool VEC>
-__device__ __forceinline__ void load_iter(const double* x, int V, int base, RawIter<double>& r) {
-  const int off = lane_off(base);
-  const bool full = VEC && base + kIterLen <= V;
-#pragma unroll
-  for (int j = 0; j < kU; ++j) {
-    const int p = off + j * 256;
-    if (full || (VEC && p + 3 < V)) {
-      r.v[2 * j] = __builtin_nontemporal_load(reinterpret_cast<const d2_t*>(x + p));
-      r.v[2 * j + 1] = __builtin_nontemporal_load(reinterpret_cast<const d2_t*>(x + p + 2));
-    } else {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) r.v[2 * j + (s >> 1)][s & 1] = (p + s < V) ? x[p + s] : -INFINITY;
-    }
-  }
-}
-
-__device__ __forceinline__ double raw_at(const RawIter<float>& r, int e) { return (double)r.v[e >> 2][e & 3]; }
-__device__ __forceinline__ double raw_at(const RawIter<double>& r, int e) { return r.v[e >> 1][e & 1]; }
-
-// Validity (bit e: token e lies inside the row) and penalty (bit e: token e
-// is in the history) masks of the calling lane for the iteration at `base`.
-__device__ __forceinline__ void lane_bits(int base, int V, const RowParams& rp, const uint32_t* bitmap,
-                                          uint32_t* vmask, uint32_t* pbits) {
-  const int off = lane_off(base);
-  uint32_t m = 0, pb = 0;
-#pragma unroll
-  for (int e = 0; e < kE; ++e)
-    if (off + (e >> 2) * 256 + (e & 3) < V) m |= 1u << e;
-  if (rp.pen_active) {
-#pragma unroll
-    for (int j = 0; j < kU; ++j) {
-      const int p = off + j * 256;
-      if (p < V) pb |= ((bitmap[p >> 5] >> (p & 31)) & 0xFu) << (4 * j);
-    }
-  }
-  *vmask = m;
-  *pbits = pb;
-}
-
-// Penalised logit of register slot e.
-template <typename TIn>
-__device__ __forceinline__ double zat(const RawIter<TIn>& r, int e, uint32_t pbits, double pen) {
-  const double v = raw_at(r, e);
-  return ((pbits >> e) & 1u) ? penalize(v, pen) : v;
-}
-
-__device__ __forceinline__ int tok_idx(int base, int e) { return lane_off(base) + (e >> 2) * 256 + (e & 3); }
-
 // y = z / T as the segment partials compute it (multiplication by 1/T).
 struct YScale {
   double T, invT;
   __device__ __forceinline__ double operator()(double z) const { return T == 1.0 ? z : z * invT; }
 };
 
-// Wave-wide softmax partial of one 2048-token segment: (max y, sum exp(y - max y)).
-template <typename TIn>
-__device__ __forceinline__ void segment_partial(const RawIter<TIn>& r, uint32_t vmask, uint32_t pbits, double pen,
-                                                const YScale& ys, const double* tab, double* seg_m, double* seg_s,
-                                                int seg) {
-  double m = -INFINITY;
-#pragma unroll
-  for (int e = 0; e < kE; ++e)
-    if ((vmask >> e) & 1u) m = fmax(m, ys(zat(r, e, pbits, pen)));
-  m = wave_max(m);
-  double s = 0.0;
-  if (m > -INFINITY) {
-#pragma unroll
-    for (int e = 0; e < kE; ++e)
-      if ((vmask >> e) & 1u) s += fast_exp_neg(ys(zat(r, e, pbits, pen)) - m, tab);
-  }
-  s = wave_sum(s);
-  if (lane() == 0) {
-    seg_m[seg] = m;
-    seg_s[seg] = s;
-  }
-}
+// ================================================================ chunks
 
-// ------------------------------------------------------------- selection
-
-// The smallest value of the histogram bin that holds the target-th largest
-// of the valid finite z in registers (-inf if there are fewer than target).
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef double d2_t __attribute__((ext_vector_type(2)));
 template <typename TIn>
-__device__ __forceinline__ double theta_from_regs(const RawIter<TIn>& r, uint32_t vmask, uint32_t pbits, double pen,
-                                                  uint64_t target, FastSmem& fs) {
-  double lo = INFINITY, hi = -INFINITY;
-#pragma unroll
-  for (int e = 0; e < kE; ++e) {
-    const double z = zat(r, e, pbits, pen);
-    if (((vmask >> e) & 1u) && z > -INFINITY) {
-      lo = fmin(lo, z);
-      hi = fmax(hi, z);
-    }
-  }
-  lo = block_min(lo, fs.redd);
-  hi = block_max(hi, fs.redd);
-  if (!(hi > -INFINITY)) return -INFINITY;
-  const Affine af = make_affine(lo, hi, kHB);
-  for (int b = threadIdx.x; b < kHB; b += kThreads) fs.hcnt[b] = 0u;
-  lds_barrier();
-#pragma unroll
-  for (int e = 0; e < kE; ++e) {
-    const double z = zat(r, e, pbits, pen);
-    if (((vmask >> e) & 1u) && z > -INFINITY) lds_add(&fs.hcnt[af.bin(z)], 1u);
-  }
-  lds_barrier();
-  const Pick pk = pick_desc<false>(fs.hcnt, fs.hmass, kHB, 0, target, fs.redu, fs.ctl, fs.ctlu);
-  if (!pk.found) return -INFINITY;
-  double m = INFINITY;
-#pragma unroll
-  for (int e = 0; e < kE; ++e) {
-    const double z = zat(r, e, pbits, pen);
-    if (((vmask >> e) & 1u) && z > -INFINITY && af.bin(z) == pk.d) m = fmin(m, z);
-  }
-  return block_min(m, fs.redd);
-}
-
-// Candidate store: value (the input type) and index, bit 31 set when the
-// token's penalty applies.
-template <typename TIn>
-struct Cands {
-  TIn* val;
-  int* code;
-  int cap;
-  __device__ __forceinline__ double z(int c, double pen) const {
-    double v = (double)val[c];
-    return code[c] < 0 ? penalize(v, pen) : v;
-  }
-  __device__ __forceinline__ int idx(int c) const { return code[c] & 0x7fffffff; }
+struct VecOf;
+template <>
+struct VecOf<float> {
+  typedef f4_t T;
+};
+template <>
+struct VecOf<double> {
+  typedef d2_t T;
 };
 
-// Keep the candidates >= the smallest value of the histogram bin holding
-// the target-th largest; in-place stable compaction, one round of kThreads
-// entries at a time (a kept entry only moves down, into rounds already
-// read).  Returns the new threshold; *umax gets the dropped maximum.
+struct ChunkSmem {
+  double redd[2 * kWaves];
+  uint64_t redu[kWaves];
+  int redi[kWaves];
+  int ctl[8];
+  uint64_t ctlu[4];
+  double exp_tab[64];
+  uint32_t hcnt[kHB];
+  uint32_t bitmap[Geo<float>::kChunk / 32];
+  int cand_n;
+};
+
+// Chunk-local offset of the calling lane's register slot e: the lane's
+// j-th load (j = e / kVW) covers kVW consecutive tokens at
+// wave*kSeg + j*kSpan + lane*kVW, so each load instruction of a wave reads
+// 1 KB of contiguous HBM.
 template <typename TIn>
-__device__ __forceinline__ double compact_cands(const Cands<TIn>& cs, uint64_t target, double pen, double* umax,
-                                                FastSmem& fs) {
-  const int n = min(fs.cand_n, cs.cap);
-  double lo = INFINITY, hi = -INFINITY;
-  for (int c = threadIdx.x; c < n; c += kThreads) {
-    const double z = cs.z(c, pen);
-    if (z > -INFINITY) {
-      lo = fmin(lo, z);
-      hi = fmax(hi, z);
-    }
-  }
-  lo = block_min(lo, fs.redd);
-  hi = block_max(hi, fs.redd);
-  const Affine af = make_affine(lo, hi, kHB);
-  for (int b = threadIdx.x; b < kHB; b += kThreads) fs.hcnt[b] = 0u;
-  lds_barrier();
-  for (int c = threadIdx.x; c < n; c += kThreads) {
-    const double z = cs.z(c, pen);
-    if (z > -INFINITY) lds_add(&fs.hcnt[af.bin(z)], 1u);
-  }
-  lds_barrier();
-  const Pick pk = pick_desc<false>(fs.hcnt, fs.hmass, kHB, 0, target, fs.redu, fs.ctl, fs.ctlu);
-  double theta = -INFINITY;
-  if (pk.found) {
-    double m = INFINITY;
-    for (int c = threadIdx.x; c < n; c += kThreads) {
-      const double z = cs.z(c, pen);
-      if (z > -INFINITY && af.bin(z) == pk.d) m = fmin(m, z);
-    }
-    theta = block_min(m, fs.redd);
-  }
-  int kept = 0;
-  for (int r0 = 0; r0 < n; r0 += kThreads) {
-    const int c = r0 + threadIdx.x;
-    TIn v = TIn(0);
-    int code = 0;
-    bool keep = false;
-    if (c < n) {
-      v = cs.val[c];
-      code = cs.code[c];
-      const double z = cs.z(c, pen);
-      keep = z >= theta;
-      if (!keep) *umax = fmax(*umax, z);
-    }
-    uint32_t tot;
-    const uint32_t ex = block_excl_scan<uint32_t>(keep ? 1u : 0u, reinterpret_cast<uint32_t*>(fs.redu), &tot);
-    if (keep) {
-      cs.val[kept + ex] = v;
-      cs.code[kept + ex] = code;
-    }
-    kept += (int)tot;
-    lds_barrier();
-  }
-  if (threadIdx.x == 0) fs.cand_n = kept;
-  lds_barrier();
-  return theta;
+__device__ __forceinline__ int slot_q(int e) {
+  using G = Geo<TIn>;
+  return wave() * G::kSeg + (e / G::kVW) * G::kSpan + lane() * G::kVW + (e % G::kVW);
 }
 
-
-// Appends the valid tokens with z >= theta (one LDS atomic per wave and
-// register slot).  Tokens that find the store full count as dropped.
-template <typename TIn>
-__device__ __forceinline__ void insert_cands(const Cands<TIn>& cs, const RawIter<TIn>& raw, uint32_t vmask,
-                                             uint32_t pbits, double pen, int base, double theta, double* umax,
-                                             FastSmem& fs) {
-  const int off = lane_off(base);
+template <typename TIn, bool VEC>
+__device__ __forceinline__ void load_chunk(const TIn* x, int V, int c0, typename VecOf<TIn>::T (&v)[kU]) {
+  using G = Geo<TIn>;
+  using VT = typename VecOf<TIn>::T;
+  const int off = c0 + wave() * G::kSeg + lane() * G::kVW;
+  const bool full = VEC && c0 + G::kChunk <= V;  // uniform: no bounds checks needed
 #pragma unroll
-  for (int e = 0; e < kE; ++e) {
-    const double z = zat(raw, e, pbits, pen);
-    const bool valid = (vmask >> e) & 1u;
-    const bool pass = valid && z >= theta;
-    const uint64_t mask = __ballot(pass);
-    if (mask) {
-      int first = 0;
-      if (lane() == 0) first = lds_fetch_add(&fs.cand_n, (int)__popcll(mask));
-      first = __shfl(first, 0);
-      if (pass) {
-        const int slot = first + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
-                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
-        if (slot < cs.cap) {
-          if constexpr (sizeof(TIn) == 4) cs.val[slot] = raw.v[e >> 2][e & 3];
-          else cs.val[slot] = raw.v[e >> 1][e & 1];
-          cs.code[slot] = (off + (e >> 2) * 256 + (e & 3)) | (((pbits >> e) & 1u) ? (int)0x80000000 : 0);
-        } else {
-          *umax = fmax(*umax, z);
-        }
-      }
+  for (int j = 0; j < kU; ++j) {
+    const int p = off + j * G::kSpan;
+    if (full || (VEC && p + G::kVW <= V)) {
+      v[j] = __builtin_nontemporal_load(reinterpret_cast<const VT*>(x + p));
+    } else {
+#pragma unroll
+      for (int s = 0; s < G::kVW; ++s) v[j][s] = (p + s < V) ? x[p + s] : (TIn)(-INFINITY);
     }
-    if (valid && !pass) *umax = fmax(*umax, z);
   }
 }
+
+// One bit per distinct history id inside the chunk (np.unique,
+// sampling.py:59), then the calling lane's bits in register-slot order.
+template <typename TIn>
+__device__ __forceinline__ uint32_t chunk_pbits(const SampleArgs& a, const RowParams& rp, int c0, ChunkSmem& cm) {
+  using G = Geo<TIn>;
+  constexpr int kWords = G::kChunk / 32;
+  for (int w = threadIdx.x; w < kWords; w += kThreads) cm.bitmap[w] = 0u;
+  lds_barrier();
+  for (int64_t h = rp.h0 + threadIdx.x; h < rp.h1; h += kThreads) {
+    const int off = a.hist_ids[h] - c0;
+    if ((unsigned)off < (unsigned)G::kChunk) lds_or(&cm.bitmap[off >> 5], 1u << (off & 31));
+  }
+  lds_barrier();
+  uint32_t pb = 0;
+  const int q0 = wave() * G::kSeg + lane() * G::kVW;
+#pragma unroll
+  for (int j = 0; j < kU; ++j) {
+    const int q = q0 + j * G::kSpan;
+    pb |= ((cm.bitmap[q >> 5] >> (q & 31)) & ((1u << G::kVW) - 1u)) << (G::kVW * j);
+  }
+  return pb;
+}
+
+__device__ __forceinline__ void block_minmax(double* lo, double* hi, double* red) {
+  double a = wave_min(*lo), b = wave_max(*hi);
+  if (lane() == 0) {
+    red[wave()] = a;
+    red[kWaves + wave()] = b;
+  }
+  __syncthreads();
+  a = red[0];
+  b = red[kWaves];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    a = fmin(a, red[w]);
+    b = fmax(b, red[kWaves + w]);
+  }
+  __syncthreads();
+  *lo = a;
+  *hi = b;
+}
+
+// Candidates of one chunk: every finite z >= theta, where theta is the
+// lower edge of the value-histogram bin that holds the target-th largest
+// (all finite tokens when there are fewer).  Writes them to the chunk's
+// workspace slots; the largest finite z not written goes to part->umax.
+template <typename TIn>
+__device__ __forceinline__ void chunk_candidates(const double (&z)[Geo<TIn>::kEpt], const SampleArgs& a,
+                                                 const RowParams& rp, int c0, ChunkSmem& cm) {
+  constexpr int kEpt = Geo<TIn>::kEpt;
+  const int capc = a.ws.capc;
+  // top-p rows keep as many as the slots allow, less a margin for the
+  // histogram bin that straddles the threshold
+  const uint64_t keep = (uint64_t)(capc - capc / 16);
+  const uint64_t target = rp.topk ? min((uint64_t)rp.top_k, keep) : keep;
+  double lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < kEpt; ++e)
+    if (z[e] > -INFINITY) {
+      lo = fmin(lo, z[e]);
+      hi = fmax(hi, z[e]);
+    }
+  block_minmax(&lo, &hi, cm.redd);
+  double theta = -INFINITY;
+  if (hi > -INFINITY) {
+    const Affine af = make_affine(lo, hi, kHB);
+    for (int b = threadIdx.x; b < kHB; b += kThreads) cm.hcnt[b] = 0u;
+    lds_barrier();
+#pragma unroll
+    for (int e = 0; e < kEpt; ++e)
+      if (z[e] > -INFINITY) lds_add(&cm.hcnt[af.bin(z[e])], 1u);
+    lds_barrier();
+    const Pick pk = pick_desc<false>(cm.hcnt, nullptr, kHB, 0, target, cm.redu, cm.ctl, cm.ctlu);
+    // every z with bin(z) >= d is >= lo + (d - 0.01) / scale (bin(z) is
+    // floor((z - lo) * scale) up to a few ulps)
+    if (pk.found && pk.d > 0) theta = af.lo + ((double)pk.d - 0.01) / af.scale;
+  }
+  uint32_t pm = 0;
+  double um = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < kEpt; ++e) {
+    const bool fin = z[e] > -INFINITY;
+    if (fin && z[e] >= theta) pm |= 1u << e;
+    else if (fin) um = fmax(um, z[e]);
+  }
+  // one LDS reservation per wave
+  const int cnt = __popc(pm);
+  int incl = cnt;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(incl, off);
+    if (lane() >= off) incl += y;
+  }
+  int base = 0;
+  if (lane() == kWave - 1) base = lds_fetch_add(&cm.cand_n, incl);
+  base = __shfl(base, kWave - 1);
+  int slot = base + incl - cnt;
+  double* cz = a.ws.cz + (size_t)blockIdx.x * capc;
+  int32_t* ci = a.ws.ci + (size_t)blockIdx.x * capc;
+#pragma unroll
+  for (int e = 0; e < kEpt; ++e) {
+    if ((pm >> e) & 1u) {
+      if (slot < capc) {
+        cz[slot] = z[e];
+        ci[slot] = c0 + slot_q<TIn>(e);
+      } else {
+        um = fmax(um, z[e]);
+      }
+      ++slot;
+    }
+  }
+  um = block_max(um, cm.redd);
+  if (threadIdx.x == 0) {
+    ChunkPart* part = a.ws.part + blockIdx.x;
+    part->zmax = hi;
+    part->umax = um;
+    part->n = min(cm.cand_n, capc);
+  }
+}
+
+template <typename TIn, bool VEC>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_sample_chunks(SampleArgs a) {
+  using G = Geo<TIn>;
+  __shared__ ChunkSmem cm;
+  const int C = a.ws.C;
+  const int row = blockIdx.x / C;
+  const int c0 = (blockIdx.x - row * C) * G::kChunk;
+  const RowParams rp = load_row_params(a, row);
+  const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
+  typename VecOf<TIn>::T v[kU];
+  load_chunk<TIn, VEC>(x, a.V, c0, v);
+  init_exp_table(cm.exp_tab);
+  if (threadIdx.x == 0) cm.cand_n = 0;
+  const uint32_t pb = rp.pen_active ? chunk_pbits<TIn>(a, rp, c0, cm) : 0u;
+  lds_barrier();
+  double z[G::kEpt];
+#pragma unroll
+  for (int e = 0; e < G::kEpt; ++e) z[e] = (double)v[e / G::kVW][e % G::kVW];
+  if (pb != 0u) {
+#pragma unroll
+    for (int e = 0; e < G::kEpt; ++e)
+      if ((pb >> e) & 1u) z[e] = penalize(z[e], rp.pen);
+  }
+  if (rp.greedy) {
+    ArgMax best{-INFINITY, INT_MAX};
+#pragma unroll
+    for (int e = 0; e < G::kEpt; ++e) best = argmax_merge(best, ArgMax{z[e], c0 + slot_q<TIn>(e)});
+    best = block_argmax(best, cm.redd, cm.redi);
+    if (threadIdx.x == 0) {
+      a.ws.part[blockIdx.x].best_z = best.v;
+      a.ws.part[blockIdx.x].best_idx = best.i;
+    }
+    return;
+  }
+  // candidates first: the segment pass below is then the last use of z
+  if (rp.topk || rp.topp) chunk_candidates<TIn>(z, a, rp, c0, cm);
+  if (!rp.topk) {  // the full-vocabulary normaliser (sampling.py:79-81)
+    const YScale ys{rp.T, 1.0 / rp.T};
+    double m = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < G::kEpt; ++e) m = fmax(m, ys(z[e]));
+    m = wave_max(m);
+    double s = 0.0;
+    if (m > -INFINITY) {
+#pragma unroll
+      for (int e = 0; e < G::kEpt; ++e) s += fast_exp_neg(ys(z[e]) - m, cm.exp_tab);
+    }
+    s = wave_sum(s);
+    if (lane() == 0) {
+      a.ws.seg_m[(size_t)blockIdx.x * kWaves + wave()] = m;
+      a.ws.seg_s[(size_t)blockIdx.x * kWaves + wave()] = s;
+    }
+  }
+}
+
+// ================================================================ finish
 
 // Inclusive and exclusive scan of one double per thread, thread order,
 // fixed association.
@@ -409,6 +393,13 @@ __device__ __forceinline__ double block_scan_d(double v, double* red, double* ex
   return pre + x;
 }
 
+// Candidate store in LDS: penalised logit and token id.
+struct Cands {
+  const double* z;
+  const int* ix;
+  __device__ __forceinline__ int idx(int c) const { return ix[c]; }
+};
+
 // Value-range selection over the candidate store: candidates with elig(c)
 // take part; val(c) places them in histogram bins (monotone in the order),
 // key(c) orders them exactly, token index ascending on equal keys.
@@ -424,8 +415,8 @@ struct SelOut {
   int idx;
 };
 
-template <bool MASS, typename TIn, class Elig, class Val, class Key, class W>
-__device__ __forceinline__ SelOut cand_select(const Cands<TIn>& cs, int n, const Elig& elig, const Val& val,
+template <bool MASS, class Elig, class Val, class Key, class W>
+__device__ __forceinline__ SelOut cand_select(const Cands& cs, int n, const Elig& elig, const Val& val,
                                               const Key& key, const W& wt, uint64_t target, FastSmem& fs) {
   Affine lv[kSelLevels];
   int dv[kSelLevels];
@@ -523,8 +514,8 @@ __device__ __forceinline__ SelOut cand_select(const Cands<TIn>& cs, int n, const
 // (sampling.py:94-98): with w(c) the fixed-point probability of kept
 // candidates (0 otherwise), the first token whose running mass exceeds
 // floor(u * total); V-1 when none does.
-template <typename TIn, class W>
-__device__ __forceinline__ int draw_kept(const Cands<TIn>& cs, int n, int V, double u, const W& wt, FastSmem& fs) {
+template <class W>
+__device__ __forceinline__ int draw_kept(const Cands& cs, int n, int V, double u, const W& wt, FastSmem& fs) {
   uint64_t tot = 0;
   for (int c = threadIdx.x; c < n; c += kThreads) tot += wt(c);
   tot = block_sum<uint64_t>(tot, fs.redu);
@@ -587,67 +578,76 @@ __device__ __forceinline__ int draw_kept(const Cands<TIn>& cs, int n, int V, dou
   return hit == INT_MAX ? V - 1 : hit;
 }
 
-// ------------------------------------------------------------ row modes
-
-template <typename TIn, bool VEC>
-__device__ __forceinline__ int run_greedy(const TIn* x, int V, const RowParams& rp, FastSmem& fs) {
-  RawIter<TIn> cur, nxt;
-  load_iter<VEC>(x, V, 0, cur);
+// Greedy rows: argmax over the chunk argmaxes (lowest index on ties).
+__device__ __forceinline__ int finish_greedy(const SampleArgs& a, int row, FastSmem& fs) {
+  const int C = a.ws.C;
   ArgMax best{-INFINITY, INT_MAX};
-  for (int base = 0; base < V; base += kIterLen) {
-    if (base + kIterLen < V) load_iter<VEC>(x, V, base + kIterLen, nxt);
-    uint32_t vm, pb;
-    lane_bits(base, V, rp, fs.u.bitmap, &vm, &pb);
-#pragma unroll
-    for (int e = 0; e < kE; ++e)
-      if ((vm >> e) & 1u) best = argmax_merge(best, ArgMax{zat(cur, e, pb, rp.pen), tok_idx(base, e)});
-    cur = nxt;
+  for (int c = threadIdx.x; c < C; c += kThreads) {
+    const ChunkPart& p = a.ws.part[(size_t)row * C + c];
+    best = argmax_merge(best, ArgMax{p.best_z, p.best_idx});
   }
-  best = block_argmax(best, fs.redd, fs.redi);
-  return best.i;
+  return block_argmax(best, fs.redd, fs.redi).i;
 }
 
-// Temperature only: full-vocabulary softmax and draw (sampling.py:75-81, :94-98).
-template <typename TIn, bool VEC>
-__device__ __forceinline__ int run_temp(const TIn* x, int V, const RowParams& rp, FastSmem& fs) {
-  const YScale ys{rp.T, 1.0 / rp.T};
-  RawIter<TIn> cur, nxt;
-  load_iter<VEC>(x, V, 0, cur);
-  for (int base = 0; base < V; base += kIterLen) {
-    if (base + kIterLen < V) load_iter<VEC>(x, V, base + kIterLen, nxt);
-    uint32_t vm, pb;
-    lane_bits(base, V, rp, fs.u.bitmap, &vm, &pb);
-    segment_partial(cur, vm, pb, rp.pen, ys, fs.exp_tab, fs.seg_m, fs.seg_s, base / kSegLen + wave());
-    cur = nxt;
-  }
-  lds_barrier();
-  const int nseg = (V + kSegLen - 1) / kSegLen;
+// The full distribution's segment partials, one per thread (nseg <=
+// kThreads): *mk the segment max, *mass its sum rescaled to the largest
+// segment max, which goes to *ymax.
+__device__ __forceinline__ void segment_masses(const SampleArgs& a, int row, int nseg, FastSmem& fs, double* ymax,
+                                               double* mk, double* mass) {
   const int k = threadIdx.x;
-  const double mk = k < nseg ? fs.seg_m[k] : -INFINITY;
-  const double ymax = block_max(mk, fs.redd);
-  const double mass = (k < nseg && mk > -INFINITY) ? fs.seg_s[k] * fast_exp_neg(mk - ymax, fs.exp_tab) : 0.0;
+  const size_t b = (size_t)row * a.ws.C * kWaves;
+  *mk = k < nseg ? a.ws.seg_m[b + k] : -INFINITY;
+  const double sk = k < nseg ? a.ws.seg_s[b + k] : 0.0;
+  *ymax = block_max(*mk, fs.redd);
+  *mass = (k < nseg && *mk > -INFINITY) ? sk * fast_exp_neg(*mk - *ymax, fs.exp_tab) : 0.0;
+}
+
+// Temperature only: full-vocabulary softmax and draw (sampling.py:75-81,
+// :94-98).  The segment holding the inverse-CDF point is rescanned from HBM
+// with the arithmetic of the partials.
+template <typename TIn>
+__device__ __forceinline__ int finish_temp(const SampleArgs& a, int row, const RowParams& rp, FastSmem& fs) {
+  using G = Geo<TIn>;
+  const int V = a.V;
+  const int nseg = (V + G::kSeg - 1) / G::kSeg;  // <= kThreads
+  const YScale ys{rp.T, 1.0 / rp.T};
+  const int k = threadIdx.x;
+  double ymax, mk, mass;
+  segment_masses(a, row, nseg, fs, &ymax, &mk, &mass);
   double ex, S;
   block_scan_d(mass, fs.redd, &ex, &S);
   const double t = rp.u * S;
   const int kstar = block_min<int>((k < nseg && ex + mass > t) ? k : INT_MAX, fs.redi);
   if (kstar == INT_MAX) return V - 1;
-  if (k == kstar) fs.ctlu[0] = (uint64_t)__double_as_longlong(ex);
-  lds_barrier();
+  if (k == kstar) {
+    fs.ctlu[0] = (uint64_t)__double_as_longlong(ex);
+    fs.ctlu[1] = (uint64_t)__double_as_longlong(mk);
+  }
+  const int s0 = kstar * G::kSeg;
+  if (rp.pen_active) {
+    for (int w = threadIdx.x; w < G::kSeg / 32; w += kThreads) fs.u.segbits[w] = 0u;
+    __syncthreads();
+    for (int64_t h = rp.h0 + threadIdx.x; h < rp.h1; h += kThreads) {
+      const int off = a.hist_ids[h] - s0;
+      if ((unsigned)off < (unsigned)G::kSeg) lds_or(&fs.u.segbits[off >> 5], 1u << (off & 31));
+    }
+  }
+  __syncthreads();
   const double before = __longlong_as_double((long long)fs.ctlu[0]);
-  const double ms = fs.seg_m[kstar];
+  const double ms = __longlong_as_double((long long)fs.ctlu[1]);
   const double sc = fast_exp_neg(ms - ymax, fs.exp_tab);
-  // rescan the segment with the stream's arithmetic: thread t holds tokens
-  // kstar*kSegLen + kPer*t + q, in vocabulary order
-  constexpr int kPer = kSegLen / kThreads;
-  const int p0 = kstar * kSegLen + kPer * (int)threadIdx.x;
+  // thread t holds tokens s0 + kPer*t + q, in vocabulary order
+  constexpr int kPer = G::kSeg / kThreads;
+  const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
+  const int q0 = kPer * (int)threadIdx.x;
   double e[kPer], es = 0.0;
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
     e[q] = 0.0;
-    const int pos = p0 + q;
+    const int pos = s0 + q0 + q;
     if (pos < V) {
       double z = (double)x[pos];
-      if (rp.pen_active && ((fs.u.bitmap[pos >> 5] >> (pos & 31)) & 1u)) z = penalize(z, rp.pen);
+      if (rp.pen_active && ((fs.u.segbits[(q0 + q) >> 5] >> ((q0 + q) & 31)) & 1u)) z = penalize(z, rp.pen);
       e[q] = fast_exp_neg(ys(z) - ms, fs.exp_tab);
     }
     es += e[q];
@@ -659,8 +659,8 @@ __device__ __forceinline__ int run_temp(const TIn* x, int V, const RowParams& rp
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
     run += e[q];
-    if (e[q] > 0.0) last = p0 + q;
-    if (hit == INT_MAX && e[q] > 0.0 && before + run * sc > t) hit = p0 + q;
+    if (e[q] > 0.0) last = s0 + q0 + q;
+    if (hit == INT_MAX && e[q] > 0.0 && before + run * sc > t) hit = s0 + q0 + q;
   }
   hit = block_min<int>(hit, fs.redi);
   if (hit == INT_MAX) hit = block_max<int>(last, fs.redi);  // rounding at the segment end
@@ -672,63 +672,68 @@ struct FastOut {
   bool general;  // the candidates cannot decide the row exactly
 };
 
-// Top-k and/or top-p rows (sampling.py:75-90, :94-98).
-template <typename TIn, bool VEC, bool TOPK>
-__device__ __forceinline__ FastOut run_cands(const TIn* x, int V, const RowParams& rp, FastSmem& fs) {
-  constexpr int cap = cand_cap<TIn>();
-  const Cands<TIn> cs{reinterpret_cast<TIn*>(fs.cand), reinterpret_cast<int*>(fs.cand + cap * sizeof(TIn)), cap};
-  const YScale ys{rp.T, 1.0 / rp.T};
-  constexpr bool topk = TOPK;
-  // top-k keeps a running lower bound of the k-th largest; top-p keeps the
-  // largest tokens, a count projected from the first iteration to ~0.7 cap
-  const uint64_t keep_target = topk ? (uint64_t)rp.top_k : (uint64_t)(cap * 7 / 10);
-  const uint64_t first_target =
-      topk ? (uint64_t)rp.top_k
-           : (V <= kIterLen ? keep_target : (uint64_t)max(1, (int)((double)keep_target * kIterLen / V)));
-  double theta, umax = -INFINITY, zmax_l = -INFINITY;
-  RawIter<TIn> cur, nxt;
-  load_iter<VEC>(x, V, 0, cur);
-  {  // threshold from the first iteration
-    uint32_t vm, pb;
-    lane_bits(0, V, rp, fs.u.bitmap, &vm, &pb);
-    theta = theta_from_regs(cur, vm, pb, rp.pen, first_target, fs);
+// Top-k and/or top-p rows (sampling.py:75-90, :94-98) from the gathered
+// chunk candidates.
+template <typename TIn, bool TOPK>
+__device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, int row, const RowParams& rp, FastSmem& fs) {
+  using G = Geo<TIn>;
+  const int V = a.V;
+  const int C = a.ws.C, capc = a.ws.capc;
+  double u_l = -INFINITY, zm_l = -INFINITY;
+  if ((int)threadIdx.x < C) {
+    const ChunkPart p = a.ws.part[(size_t)row * C + threadIdx.x];
+    fs.cnt_c[threadIdx.x] = p.n;
+    u_l = p.umax;
+    zm_l = p.zmax;
   }
-  for (int base = 0; base < V; base += kIterLen) {
-    if (base + kIterLen < V) load_iter<VEC>(x, V, base + kIterLen, nxt);
-    uint32_t vm, pb;
-    lane_bits(base, V, rp, fs.u.bitmap, &vm, &pb);
+  const double U = block_max(u_l, fs.redd);
+  const double zmax = block_max(zm_l, fs.redd);
+  // gather: thread t reads slots [16t, 16t + 16) of the row's C * capc slots
+  constexpr int kPerT = kCandCap / kThreads;
+  const int s0 = kPerT * (int)threadIdx.x;
+  int mine = 0;
+  double zl[kPerT];
+  int il[kPerT];
+  if (s0 < C * capc) {
+    const int c = s0 / capc, l0 = s0 - c * capc;
+    mine = min(max(fs.cnt_c[c] - l0, 0), kPerT);
+    const size_t g = ((size_t)row * C + c) * capc + l0;
 #pragma unroll
-    for (int e = 0; e < kE; ++e)
-      if ((vm >> e) & 1u) zmax_l = fmax(zmax_l, zat(cur, e, pb, rp.pen));
-    if constexpr (!topk) segment_partial(cur, vm, pb, rp.pen, ys, fs.exp_tab, fs.seg_m, fs.seg_s, base / kSegLen + wave());
-    insert_cands(cs, cur, vm, pb, rp.pen, base, theta, &umax, fs);
-    cur = nxt;
-    lds_barrier();
-    if (fs.cand_n > cap - 2048) theta = fmax(theta, compact_cands(cs, keep_target, rp.pen, &umax, fs));
+    for (int q = 0; q < kPerT; ++q)
+      if (q < mine) {
+        zl[q] = a.ws.cz[g + q];
+        il[q] = a.ws.ci[g + q];
+      }
   }
-  lds_barrier();
-  const int n = min(fs.cand_n, cap);
-  const double U = block_max(umax, fs.redd);
-  const double zmax = block_max(zmax_l, fs.redd);
+  uint32_t ntot;
+  const int off = (int)block_excl_scan<uint32_t>((uint32_t)mine, reinterpret_cast<uint32_t*>(fs.redu), &ntot);
+#pragma unroll
+  for (int q = 0; q < kPerT; ++q)
+    if (q < mine) {
+      fs.cz[off + q] = zl[q];
+      fs.ci[off + q] = il[q];
+    }
+  __syncthreads();
+  const int n = (int)ntot;
+  const Cands cs{fs.cz, fs.ci};
   const double T = rp.T;
   auto yexact = [&](double z) -> double { return T == 1.0 ? z : z / T; };
   const double ymax = yexact(zmax);
-  auto zc = [&](int c) -> double { return cs.z(c, rp.pen); };
+  auto zc = [&](int c) -> double { return fs.cz[c]; };
 
   // ---- top-k: k-th largest with multiplicity, keep y >= kth_y (:76-78)
   double z_lo = -INFINITY;
-  if (topk) {
+  if (TOPK) {
     const SelOut r = cand_select<false>(cs, n, [](int) { return true; }, zc, [&](int c) { return key_of(zc(c)); },
                                         [](int) { return 0ull; }, (uint64_t)rp.top_k, fs);
     if (!r.found) return FastOut{V - 1, true};
     const double kth_z = val_of_key(r.key);
-    if (kth_z > -INFINITY) {
-      const double kth_y = yexact(kth_z);
-      z_lo = kth_z;
-      for (int it = 0; it < 64; ++it) {
-        const double zp = dbl_prev(z_lo);
-        if (yexact(zp) >= kth_y) z_lo = zp; else break;
-      }
+    const double kth_y = yexact(kth_z);
+    z_lo = kth_z;
+    for (int it = 0; it < 64; ++it) {
+      const double zp = dbl_prev(z_lo);
+      if (yexact(zp) >= kth_y) z_lo = zp;
+      else break;
     }
     if (!(U < z_lo)) return FastOut{V - 1, true};
   }
@@ -736,7 +741,7 @@ __device__ __forceinline__ FastOut run_cands(const TIn* x, int V, const RowParam
 
   // ---- softmax normaliser (:79-81)
   double S;
-  if (topk) {
+  if (TOPK) {
     double s = 0.0;
     for (int c = threadIdx.x; c < n; c += kThreads) {
       const double z = zc(c);
@@ -744,12 +749,10 @@ __device__ __forceinline__ FastOut run_cands(const TIn* x, int V, const RowParam
     }
     S = block_sum(s, fs.redd);
   } else {
-    const int nseg = (V + kSegLen - 1) / kSegLen;
-    const int k = threadIdx.x;
-    const double mk = k < nseg ? fs.seg_m[k] : -INFINITY;
-    const double ysmax = block_max(mk, fs.redd);
-    const double m = (k < nseg && mk > -INFINITY) ? fs.seg_s[k] * fast_exp_neg(mk - ysmax, fs.exp_tab) : 0.0;
-    S = block_sum(m, fs.redd);
+    const int nseg = (V + G::kSeg - 1) / G::kSeg;
+    double ysmax, mk, mass;
+    segment_masses(a, row, nseg, fs, &ysmax, &mk, &mass);
+    S = block_sum(mass, fs.redd);
   }
   auto pc = [&](int c) -> double {
     const double z = zc(c);
@@ -770,7 +773,7 @@ __device__ __forceinline__ FastOut run_cands(const TIn* x, int V, const RowParam
       cut_key = r.key;
       cut_idx = r.idx;
     }
-    if (!topk && U > -INFINITY) {
+    if (!TOPK && U > -INFINITY) {
       const double pU = fast_exp_neg(yexact(U) - ymax, fs.exp_tab) / S;
       if (!(have_cut && cut_key > pkey_of(pU))) return FastOut{V - 1, true};
     }
@@ -791,25 +794,21 @@ __device__ __forceinline__ FastOut run_cands(const TIn* x, int V, const RowParam
 }
 
 template <typename TIn, bool VEC>
-__global__ __launch_bounds__(kThreads) void k_sample_fast(SampleArgs a) {
+__global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   __shared__ SmemAll sm;
   FastSmem& fs = sm.f;
   const int row = blockIdx.x;
-  const int V = a.V;
   const RowParams rp = load_row_params(a, row);
-  const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
   init_exp_table(fs.exp_tab);
-  if (threadIdx.x == 0) fs.cand_n = 0;
-  if (rp.pen_active) build_bitmap(fs.u.bitmap, 0, V, a.hist_ids, rp.h0, rp.h1);
   __syncthreads();
   int id;
   bool general = false;
   if (rp.greedy) {
-    id = run_greedy<TIn, VEC>(x, V, rp, fs);
+    id = finish_greedy(a, row, fs);
   } else if (!rp.topk && !rp.topp) {
-    id = run_temp<TIn, VEC>(x, V, rp, fs);
+    id = finish_temp<TIn>(a, row, rp, fs);
   } else {
-    const FastOut o = rp.topk ? run_cands<TIn, VEC, true>(x, V, rp, fs) : run_cands<TIn, VEC, false>(x, V, rp, fs);
+    const FastOut o = rp.topk ? finish_cands<TIn, true>(a, row, rp, fs) : finish_cands<TIn, false>(a, row, rp, fs);
     id = o.id;
     general = o.general;
   }
@@ -866,6 +865,48 @@ __global__ __launch_bounds__(kThreads) void k_penalize(PenalizeArgs a) {
 
 // ---------------------------------------------------------------- launch
 
+namespace {
+
+int chunks_of(int V, bool f64) {
+  const int L = f64 ? Geo<double>::kChunk : Geo<float>::kChunk;
+  return (V + L - 1) / L;
+}
+
+// Candidate slots per chunk: a power of two (>= 16) with C * capc <= kCandCap.
+int capc_of(int C) {
+  int c = kCapChunk;
+  while (c > 16 && c * C > kCandCap) c >>= 1;
+  return c;
+}
+
+size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+}  // namespace
+
+size_t fast_ws_bytes(int B, int V, bool f64) {
+  const size_t C = (size_t)chunks_of(V, f64), cap = (size_t)capc_of((int)C), n = (size_t)B * C;
+  return up256(n * sizeof(ChunkPart)) + 2 * up256(n * kWaves * sizeof(double)) + up256(n * cap * sizeof(double)) +
+         up256(n * cap * sizeof(int32_t));
+}
+
+ChunkWs fast_ws_layout(void* base, int B, int V, bool f64) {
+  ChunkWs w{};
+  w.C = chunks_of(V, f64);
+  w.capc = capc_of(w.C);
+  const size_t n = (size_t)B * w.C;
+  char* p = static_cast<char*>(base);
+  w.part = reinterpret_cast<ChunkPart*>(p);
+  p += up256(n * sizeof(ChunkPart));
+  w.seg_m = reinterpret_cast<double*>(p);
+  p += up256(n * kWaves * sizeof(double));
+  w.seg_s = reinterpret_cast<double*>(p);
+  p += up256(n * kWaves * sizeof(double));
+  w.cz = reinterpret_cast<double*>(p);
+  p += up256(n * w.capc * sizeof(double));
+  w.ci = reinterpret_cast<int32_t*>(p);
+  return w;
+}
+
 hipError_t launch_sample_rows(const SampleArgs& a, bool f64, bool vec, hipStream_t s) {
   const dim3 grid(a.B), block(kThreads);
   if (f64) {
@@ -878,15 +919,18 @@ hipError_t launch_sample_rows(const SampleArgs& a, bool f64, bool vec, hipStream
   return hipGetLastError();
 }
 
-hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, hipStream_t s) {
-  const dim3 grid(a.B), block(kThreads);
-  if (f64) {
-    if (vec) hipLaunchKernelGGL((k_sample_fast<double, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((k_sample_fast<double, false>), grid, block, 0, s, a);
-  } else {
-    if (vec) hipLaunchKernelGGL((k_sample_fast<float, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((k_sample_fast<float, false>), grid, block, 0, s, a);
+hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, hipStream_t s, hipEvent_t between) {
+  const dim3 gc((unsigned)a.B * (unsigned)a.ws.C), gf(a.B), block(kThreads);
+  auto chunks = f64 ? (vec ? k_sample_chunks<double, true> : k_sample_chunks<double, false>)
+                    : (vec ? k_sample_chunks<float, true> : k_sample_chunks<float, false>);
+  auto final_ = f64 ? (vec ? k_sample_final<double, true> : k_sample_final<double, false>)
+                    : (vec ? k_sample_final<float, true> : k_sample_final<float, false>);
+  hipLaunchKernelGGL(chunks, gc, block, 0, s, a);
+  if (between != nullptr) {
+    const hipError_t e = hipEventRecord(between, s);
+    if (e != hipSuccess) return e;
   }
+  hipLaunchKernelGGL(final_, gf, block, 0, s, a);
   return hipGetLastError();
 }
 
