@@ -1,14 +1,23 @@
 // Device primitives shared by the gfx950 sampler kernels: order-preserving
 // keys, fixed-point masses, wave64/workgroup reductions and scans.
 //
-// Every reduction and scan here combines values in a fixed order (xor
-// butterflies inside a wave, then the waves' partials left to right), so the
+// Every reduction and scan here combines values in a fixed order (a DPP
+// scan inside each wave, then the waves' partials left to right), so the
 // kernels are deterministic run to run.  Integer (fixed-point) scans are
 // exact, which is what the inverse-CDF draws and the top-p mass selection
 // rely on.
+//
+// Cross-lane steps use DPP (data-parallel primitives: a VALU operand read
+// from another lane of the same instruction) rather than ds_bpermute, whose
+// every step is an LDS round trip.  The wave64 scan is the gfx9 sequence:
+// row_shr 1, 2, 4, 8 inside each row of 16 lanes, then row_bcast15 into rows
+// 1 and 3 and row_bcast31 into rows 2 and 3; lane 63 then holds the total.
+// Callers invoke these from converged code (all 64 lanes active).
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <limits.h>
+#include <math.h>
 #include <stdint.h>
 
 namespace plh {
@@ -52,6 +61,13 @@ __device__ __forceinline__ uint64_t to_fx(double p) {
   return p > 0.0 ? (uint64_t)__double2ull_rn(p * kFxScale) : 0ull;
 }
 
+// Fixed-point top-p target, at least 1 so that a top_p below 2^-62 still
+// keeps the first token (its inclusive mass reaches any positive top_p).
+__device__ __forceinline__ uint64_t topp_target(double top_p) {
+  const uint64_t t = to_fx(top_p);
+  return t > 0 ? t : 1ull;
+}
+
 // Largest double strictly below d (d finite).
 __device__ __forceinline__ double dbl_prev(double d) {
   if (d == 0.0) return -4.9406564584124654e-324;
@@ -92,31 +108,85 @@ __device__ __forceinline__ void glb_add(unsigned long long* p, unsigned long lon
 
 // ------------------------------------------------------------ reductions
 
+// DPP controls (gfx9 encoding).
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr4 = 0x114, kDppRowShr8 = 0x118;
+constexpr int kDppWaveShr1 = 0x138, kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+
+// One DPP move of a 4- or 8-byte value: lanes whose source is outside the
+// pattern, or whose row is not in ROWM, receive `old`.
+template <int CTRL, int ROWM, typename T>
+__device__ __forceinline__ T dpp(T old, T src) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "4- or 8-byte values");
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                             __builtin_bit_cast(int, src), CTRL, ROWM, 0xf, false));
+  } else {
+    const uint64_t o = __builtin_bit_cast(uint64_t, old), v = __builtin_bit_cast(uint64_t, src);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)o, (int)(uint32_t)v, CTRL, ROWM, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)(o >> 32), (int)(uint32_t)(v >> 32), CTRL,
+                                                              ROWM, 0xf, false);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  }
+}
+
+// Value of lane l (uniform).
+template <typename T>
+__device__ __forceinline__ T lane_value(T v, int l) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+  } else {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  }
+}
+
+// Inclusive scan over the 64 lanes with an associative op and its identity.
+template <typename T, class Op>
+__device__ __forceinline__ T wave_scan_incl(T v, T id, const Op& op) {
+  v = op(v, dpp<kDppRowShr1, 0xf>(id, v));
+  v = op(v, dpp<kDppRowShr2, 0xf>(id, v));
+  v = op(v, dpp<kDppRowShr4, 0xf>(id, v));
+  v = op(v, dpp<kDppRowShr8, 0xf>(id, v));
+  v = op(v, dpp<kDppRowBcast15, 0xa>(id, v));
+  v = op(v, dpp<kDppRowBcast31, 0xc>(id, v));
+  return v;
+}
+
+// The inclusive value of the previous lane (id for lane 0).
+template <typename T>
+__device__ __forceinline__ T wave_shift_up1(T incl, T id) {
+  return dpp<kDppWaveShr1, 0xf>(id, incl);
+}
+
+struct OpAdd {
+  template <typename T>
+  __device__ __forceinline__ T operator()(T a, T b) const { return a + b; }
+};
+struct OpMax {
+  template <typename T>
+  __device__ __forceinline__ T operator()(T a, T b) const { return b > a ? b : a; }
+};
+struct OpMin {
+  template <typename T>
+  __device__ __forceinline__ T operator()(T a, T b) const { return b < a ? b : a; }
+};
+
+// Wave reductions; every lane receives the result.
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
+  return lane_value(wave_scan_incl(v, T(0), OpAdd{}), kWave - 1);
 }
 
 template <typename T>
 __device__ __forceinline__ T wave_max(T v) {
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) {
-    const T o = __shfl_xor(v, off);
-    v = o > v ? o : v;
-  }
-  return v;
+  return lane_value(wave_scan_incl(v, v, OpMax{}), kWave - 1);
 }
 
 template <typename T>
 __device__ __forceinline__ T wave_min(T v) {
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) {
-    const T o = __shfl_xor(v, off);
-    v = o < v ? o : v;
-  }
-  return v;
+  return lane_value(wave_scan_incl(v, v, OpMin{}), kWave - 1);
 }
 
 // All threads of the workgroup receive the result.  `red` holds kWaves slots.
@@ -167,14 +237,16 @@ __device__ __forceinline__ ArgMax argmax_merge(ArgMax a, ArgMax b) {
 }
 
 __device__ __forceinline__ ArgMax block_argmax(ArgMax a, double* redd, int* redi) {
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) {
-    ArgMax o;
-    o.v = __shfl_xor(a.v, off);
-    o.i = __shfl_xor(a.i, off);
-    a = argmax_merge(a, o);
-  }
-  if (lane() == 0) {
+  // wave: a max-scan of (value, index) pairs (each DPP step moves both)
+  const ArgMax id{-INFINITY, INT_MAX};
+  auto step = [&](ArgMax o) { a = argmax_merge(a, o); };
+  step(ArgMax{dpp<kDppRowShr1, 0xf>(id.v, a.v), dpp<kDppRowShr1, 0xf>(id.i, a.i)});
+  step(ArgMax{dpp<kDppRowShr2, 0xf>(id.v, a.v), dpp<kDppRowShr2, 0xf>(id.i, a.i)});
+  step(ArgMax{dpp<kDppRowShr4, 0xf>(id.v, a.v), dpp<kDppRowShr4, 0xf>(id.i, a.i)});
+  step(ArgMax{dpp<kDppRowShr8, 0xf>(id.v, a.v), dpp<kDppRowShr8, 0xf>(id.i, a.i)});
+  step(ArgMax{dpp<kDppRowBcast15, 0xa>(id.v, a.v), dpp<kDppRowBcast15, 0xa>(id.i, a.i)});
+  step(ArgMax{dpp<kDppRowBcast31, 0xc>(id.v, a.v), dpp<kDppRowBcast31, 0xc>(id.i, a.i)});
+  if (lane() == kWave - 1) {
     redd[wave()] = a.v;
     redi[wave()] = a.i;
   }
@@ -190,12 +262,7 @@ __device__ __forceinline__ ArgMax block_argmax(ArgMax a, double* redd, int* redi
 // receives the sum over the workgroup.  Exact.
 template <typename T>
 __device__ __forceinline__ T block_excl_scan(T v, T* red, T* total) {
-  T x = v;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const T y = __shfl_up(x, off);
-    if (lane() >= off) x += y;
-  }
+  const T x = wave_scan_incl(v, T(0), OpAdd{});
   if (lane() == kWave - 1) red[wave()] = x;
   __syncthreads();
   T pre = 0, tot = 0;

@@ -1,6 +1,6 @@
-// Building blocks of the single-pass row kernel: a table-driven float64
-// exp, value-range histograms for selection, and a bitonic sort of small
-// LDS lists.
+// Building blocks of the fast path: a table-driven float64 exp, value-range
+// histograms with a descending bin walk for selection, and a bitonic sort
+// of LDS lists (used when many candidates share a value).
 #pragma once
 
 #include <limits.h>
@@ -126,28 +126,23 @@ __device__ __forceinline__ Pick pick_desc(const uint32_t* cnt, const uint64_t* m
   }
   uint64_t tot;
   const uint64_t ex = block_excl_scan<uint64_t>(s, redu, &tot);
-  if (above + tot < target) return Pick{false, -1, above + tot};
-  if (threadIdx.x == 0) ctl[0] = INT_MAX;
-  __syncthreads();
-  uint64_t run = above + ex, myrun = 0;
-  int myrank = INT_MAX;
+  if (above >= target || above + tot < target) return Pick{false, -1, above + tot};
+  // the running total is non-decreasing, so exactly one bin takes it from
+  // below target to target or more
+  uint64_t run = above + ex;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int r = (int)threadIdx.x * per + j;
-    if (j < per && r < nb && myrank == INT_MAX) {
-      if (run + v[j] >= target) {
-        myrank = r;
-        myrun = run;
+    if (j < per && r < nb) {
+      if (run < target && run + v[j] >= target) {
+        ctl[0] = nb - 1 - r;
+        ctlu[1] = run;
       }
       run += v[j];
     }
   }
-  if (myrank != INT_MAX) lds_min(&ctl[0], myrank);
   __syncthreads();
-  const int rk = ctl[0];
-  if (myrank == rk) ctlu[1] = myrun;
-  __syncthreads();
-  const Pick p{true, nb - 1 - rk, ctlu[1]};
+  const Pick p{true, ctl[0], ctlu[1]};
   __syncthreads();
   return p;
 }

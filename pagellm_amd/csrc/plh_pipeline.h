@@ -461,7 +461,7 @@ __device__ __forceinline__ PipeOut row_pipeline(Src& src, const RowParams& rp, i
   uint64_t cut_key = 0;
   int cut_idx = INT_MAX;
   if (rp.topp) {
-    const uint64_t target = to_fx(rp.top_p);
+    const uint64_t target = topp_target(rp.top_p);
     auto visit = [&](auto fn) {
       for (int base = 0; base < n; base += kTile) {
         double z[4], p[4];

@@ -62,9 +62,10 @@ struct SortList {
   int idx[kSortMax];
 };
 
-// LDS of k_sample_final (about 150 KB: one workgroup per CU).
+// LDS of k_sample_final (the candidates themselves stay in registers).
 struct FastSmem {
   double redd[kWaves];
+  double redm[2 * kWaves];
   uint64_t redu[kWaves];
   int redi[kWaves];
   int ctl[8];
@@ -77,8 +78,6 @@ struct FastSmem {
     uint32_t segbits[kSegMax / 32];  // penalty bits of the rescanned segment
     SortList sl;                     // selection and draw
   } u;
-  double cz[kCandCap];
-  int ci[kCandCap];
 };
 
 union SmemAll {
@@ -279,15 +278,10 @@ __device__ __forceinline__ void chunk_candidates(const double (&z)[Geo<TIn>::kEp
   }
   // one LDS reservation per wave
   const int cnt = __popc(pm);
-  int incl = cnt;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int y = __shfl_up(incl, off);
-    if (lane() >= off) incl += y;
-  }
+  const int incl = wave_scan_incl(cnt, 0, OpAdd{});
   int base = 0;
   if (lane() == kWave - 1) base = lds_fetch_add(&cm.cand_n, incl);
-  base = __shfl(base, kWave - 1);
+  base = lane_value(base, kWave - 1);
   int slot = base + incl - cnt;
   double* cz = a.ws.cz + (size_t)blockIdx.x * capc;
   int32_t* ci = a.ws.ci + (size_t)blockIdx.x * capc;
@@ -372,14 +366,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 // Inclusive and exclusive scan of one double per thread, thread order,
 // fixed association.
 __device__ __forceinline__ double block_scan_d(double v, double* red, double* excl, double* total) {
-  double x = v;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const double y = __shfl_up(x, off);
-    if (lane() >= off) x += y;
-  }
-  double xe = __shfl_up(x, 1);
-  if (lane() == 0) xe = 0.0;
+  const double x = wave_scan_incl(v, 0.0, OpAdd{});
+  const double xe = wave_shift_up1(x, 0.0);
   if (lane() == kWave - 1) red[wave()] = x;
   __syncthreads();
   double pre = 0.0, tot = 0.0;
@@ -393,21 +381,27 @@ __device__ __forceinline__ double block_scan_d(double v, double* red, double* ex
   return pre + x;
 }
 
-// Candidate store in LDS: penalised logit and token id.
-struct Cands {
-  const double* z;
-  const int* ix;
-  __device__ __forceinline__ int idx(int c) const { return ix[c]; }
+// Candidates of one row, held in registers: thread t owns slots
+// q * kThreads + t (q < kPerT) of the row's gathered list; bit q of `valid`
+// marks a real candidate.  v[q] holds the penalised logit, later its exp.
+constexpr int kPerT = kCandCap / kThreads;
+struct RegCands {
+  double v[kPerT];
+  int idx[kPerT];
+  uint32_t valid;
 };
 
-// Value-range selection over the candidate store: candidates with elig(c)
-// take part; val(c) places them in histogram bins (monotone in the order),
-// key(c) orders them exactly, token index ascending on equal keys.
+// Value-range selection over the register-resident candidates: slot q of
+// each thread takes part when it is valid and elig(q) holds; val(q) places
+// it in histogram bins (monotone in the order), key(q) orders exactly, token
+// index ascending on equal keys.
 //   MASS=false: the target-th largest key;
 //   MASS=true : in (key desc, index asc) order the first candidate whose
-//               inclusive weight wt(c) reaches target.
-// giveup: more than kSortMax candidates share one value at the cut (the
-// caller falls back to the general pipeline).
+//               inclusive weight wt(q) reaches target.
+// Histogram levels narrow the active set until at most 64 candidates are
+// left; one wave then ranks them (each lane counts the entries ahead of its
+// own).  giveup: more than kSortMax candidates share one value at the cut
+// (the caller falls back to the general pipeline).
 struct SelOut {
   bool found;
   bool giveup;
@@ -415,51 +409,143 @@ struct SelOut {
   int idx;
 };
 
-template <bool MASS, class Elig, class Val, class Key, class W>
-__device__ __forceinline__ SelOut cand_select(const Cands& cs, int n, const Elig& elig, const Val& val,
-                                              const Key& key, const W& wt, uint64_t target, FastSmem& fs) {
-  Affine lv[kSelLevels];
-  int dv[kSelLevels];
-  int levels = 0;
-  uint64_t above = 0;
-  auto active = [&](int c, double v) -> bool {
-    if (!elig(c)) return false;
-    for (int l = 0; l < levels; ++l)
-      if (lv[l].bin(v) != dv[l]) return false;
+// Workgroup (min, max, count) in one barrier round.
+__device__ __forceinline__ void block_range(double* lo, double* hi, uint32_t* cnt, FastSmem& fs) {
+  double a = wave_min(*lo), b = wave_max(*hi);
+  uint32_t n = wave_sum(*cnt);
+  if (lane() == 0) {
+    fs.redm[wave()] = a;
+    fs.redm[kWaves + wave()] = b;
+    reinterpret_cast<uint32_t*>(fs.redu)[wave()] = n;
+  }
+  __syncthreads();
+  a = fs.redm[0];
+  b = fs.redm[kWaves];
+  n = reinterpret_cast<uint32_t*>(fs.redu)[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    a = fmin(a, fs.redm[w]);
+    b = fmax(b, fs.redm[kWaves + w]);
+    n += reinterpret_cast<uint32_t*>(fs.redu)[w];
+  }
+  __syncthreads();
+  *lo = a;
+  *hi = b;
+  *cnt = n;
+}
+
+__device__ __forceinline__ bool key_desc_idx_asc(uint64_t ka, int ia, uint64_t kb, int ib) {
+  return ka > kb || (ka == kb && ia < ib);
+}
+
+// Histogram levels chosen so far (at most kSelLevels = 4), held in named
+// fields so they stay in registers.
+struct Levels {
+  Affine a0, a1, a2, a3;
+  int d0 = 0, d1 = 0, d2 = 0, d3 = 0;
+  int n = 0;
+  __device__ __forceinline__ bool match(double v) const {
+    if (n > 0 && a0.bin(v) != d0) return false;
+    if (n > 1 && a1.bin(v) != d1) return false;
+    if (n > 2 && a2.bin(v) != d2) return false;
+    if (n > 3 && a3.bin(v) != d3) return false;
     return true;
-  };
+  }
+  __device__ __forceinline__ void push(const Affine& a, int d) {
+    if (n == 0) {
+      a0 = a;
+      d0 = d;
+    } else if (n == 1) {
+      a1 = a;
+      d1 = d;
+    } else if (n == 2) {
+      a2 = a;
+      d2 = d;
+    } else {
+      a3 = a;
+      d3 = d;
+    }
+    ++n;
+  }
+};
+static_assert(kSelLevels == 4, "Levels holds four histogram levels");
+
+template <bool MASS, class Elig, class Val, class Key, class W>
+__device__ __forceinline__ SelOut cand_select(const RegCands& rc, const Elig& elig, const Val& val, const Key& key,
+                                              const W& wt, uint64_t target, FastSmem& fs) {
+  Levels lv;
+  uint64_t above = 0;
   SortList& sl = fs.u.sl;
   for (;;) {
     double lo = INFINITY, hi = -INFINITY;
-    uint32_t cnt = 0;
-    for (int c = threadIdx.x; c < n; c += kThreads) {
-      const double v = val(c);
-      if (active(c, v)) {
-        lo = fmin(lo, v);
-        hi = fmax(hi, v);
-        ++cnt;
-      }
-    }
-    lo = block_min(lo, fs.redd);
-    hi = block_max(hi, fs.redd);
-    cnt = block_sum<uint32_t>(cnt, reinterpret_cast<uint32_t*>(fs.redu));
-    if (cnt <= (uint32_t)kSortMax || !(hi > lo) || levels == kSelLevels) {
-      if (cnt > (uint32_t)kSortMax) return SelOut{false, true, 0, 0};
-      if (threadIdx.x == 0) fs.ctl[2] = 0;
-      lds_barrier();
-      for (int c = threadIdx.x; c < n; c += kThreads) {
-        if (active(c, val(c))) {
-          const int s = lds_fetch_add(&fs.ctl[2], 1);
-          sl.key[s] = key(c);
-          sl.idx[s] = cs.idx(c);
-          sl.w[s] = MASS ? wt(c) : 0ull;
+    uint32_t cnt = 0, act = 0;
+#pragma unroll
+    for (int q = 0; q < kPerT; ++q) {
+      if (((rc.valid >> q) & 1u) && elig(q)) {
+        const double v = val(q);
+        if (lv.match(v)) {
+          lo = fmin(lo, v);
+          hi = fmax(hi, v);
+          ++cnt;
+          act |= 1u << q;
         }
       }
+    }
+    block_range(&lo, &hi, &cnt, fs);
+    if (cnt <= (uint32_t)kWave || !(hi > lo) || lv.n == kSelLevels) {
+      if (cnt > (uint32_t)kSortMax) return SelOut{false, true, 0, 0};
+      // list the active candidates: one LDS reservation per thread
+      if (threadIdx.x == 0) fs.ctl[2] = 0;
+      lds_barrier();
+      int slot = act ? lds_fetch_add(&fs.ctl[2], __popc(act)) : 0;
+#pragma unroll
+      for (int q = 0; q < kPerT; ++q)
+        if ((act >> q) & 1u) {
+          sl.key[slot] = key(q);
+          sl.idx[slot] = rc.idx[q];
+          sl.w[slot] = MASS ? wt(q) : 0ull;
+          ++slot;
+        }
       lds_barrier();
       const int m = (int)cnt;
-      lds_bitonic(sl.key, sl.idx, sl.w, m, 0ull, [](uint64_t ka, int ia, uint64_t kb, int ib) {
-        return ka > kb || (ka == kb && ia < ib);
-      });
+      if (m <= kWave) {
+        // one wave: each lane holds one entry and counts the entries ahead of
+        // it (rank) and their weight; the answer is the lane at rank pos, or
+        // the lane whose weight takes the running total across target
+        if (wave() == 0) {
+          const int ln = lane();
+          uint64_t k = 0ull, w = 0ull;
+          int ix = INT_MAX;
+          if (ln < m) {
+            k = sl.key[ln];
+            ix = sl.idx[ln];
+            w = sl.w[ln];
+          }
+          int rank = 0;
+          uint64_t ahead = 0;
+#pragma unroll 8
+          for (int j = 0; j < m; ++j) {
+            const bool bj = key_desc_idx_asc(sl.key[j], sl.idx[j], k, ix);
+            rank += bj ? 1 : 0;
+            if (MASS && bj) ahead += sl.w[j];
+          }
+          bool hit;
+          if (!MASS) hit = ln < m && (int64_t)rank == (int64_t)target - (int64_t)above - 1;
+          else hit = ln < m && above + ahead < target && above + ahead + w >= target;
+          const uint64_t b = __ballot(hit);
+          if (ln == 0) fs.ctl[3] = b != 0 ? 1 : 0;
+          if (hit) {
+            fs.ctlu[2] = k;
+            fs.ctl[4] = ix;
+          }
+        }
+        lds_barrier();
+        const bool found = fs.ctl[3] != 0;
+        const SelOut r{found, !MASS && !found, found ? fs.ctlu[2] : 0ull, found ? fs.ctl[4] : 0};
+        lds_barrier();
+        return r;
+      }
+      lds_bitonic(sl.key, sl.idx, sl.w, m, 0ull, key_desc_idx_asc);
       if (!MASS) {
         const int pos = (int)(target - above - 1);
         if (pos < 0 || pos >= m) return SelOut{false, true, 0, 0};
@@ -492,41 +578,41 @@ __device__ __forceinline__ SelOut cand_select(const Cands& cs, int n, const Elig
       fs.hmass[b] = 0ull;
     }
     lds_barrier();
-    for (int c = threadIdx.x; c < n; c += kThreads) {
-      const double v = val(c);
-      if (active(c, v)) {
-        const int b = af.bin(v);
+#pragma unroll
+    for (int q = 0; q < kPerT; ++q)
+      if ((act >> q) & 1u) {
+        const int b = af.bin(val(q));
         lds_add(&fs.hcnt[b], 1u);
-        if (MASS) lds_add(&fs.hmass[b], wt(c));
+        if (MASS) lds_add(&fs.hmass[b], wt(q));
       }
-    }
     lds_barrier();
     const Pick pk = pick_desc<MASS>(fs.hcnt, fs.hmass, kHB, above, target, fs.redu, fs.ctl, fs.ctlu);
     if (!pk.found) return SelOut{false, false, 0, 0};
     above = pk.above;
-    lv[levels] = af;
-    dv[levels] = pk.d;
-    ++levels;
+    lv.push(af, pk.d);
   }
 }
 
 // Inverse-CDF draw over the kept candidates in vocabulary order
-// (sampling.py:94-98): with w(c) the fixed-point probability of kept
+// (sampling.py:94-98): with w(q) the fixed-point probability of kept
 // candidates (0 otherwise), the first token whose running mass exceeds
 // floor(u * total); V-1 when none does.
 template <class W>
-__device__ __forceinline__ int draw_kept(const Cands& cs, int n, int V, double u, const W& wt, FastSmem& fs) {
+__device__ __forceinline__ int draw_kept(const RegCands& rc, int V, double u, const W& wt, FastSmem& fs) {
+  auto wq = [&](int q) -> uint64_t { return ((rc.valid >> q) & 1u) ? wt(q) : 0ull; };
   uint64_t tot = 0;
-  for (int c = threadIdx.x; c < n; c += kThreads) tot += wt(c);
+#pragma unroll
+  for (int q = 0; q < kPerT; ++q) tot += wq(q);
   tot = block_sum<uint64_t>(tot, fs.redu);
   if (tot == 0) return V - 1;
   const uint64_t t = (uint64_t)__double2ull_rd(u * (double)tot);
   for (int b = threadIdx.x; b < kHB; b += kThreads) fs.hmass[b] = 0ull;
   lds_barrier();
   auto ibin = [&](int idx) -> int { return (int)(((int64_t)idx * kHB) / V); };
-  for (int c = threadIdx.x; c < n; c += kThreads) {
-    const uint64_t w = wt(c);
-    if (w) lds_add(&fs.hmass[ibin(cs.idx(c))], w);
+#pragma unroll
+  for (int q = 0; q < kPerT; ++q) {
+    const uint64_t w = wq(q);
+    if (w) lds_add(&fs.hmass[ibin(rc.idx[q])], w);
   }
   lds_barrier();
   // first index bin whose running mass exceeds t (kHB / kThreads bins per thread)
@@ -540,36 +626,62 @@ __device__ __forceinline__ int draw_kept(const Cands& cs, int n, int V, double u
   }
   uint64_t btot;
   uint64_t brun = block_excl_scan<uint64_t>(hs, fs.redu, &btot);
-  int mine = INT_MAX;
-  uint64_t mine_before = 0;
+  // the running mass is non-decreasing: one bin takes it past t
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
-    if (mine == INT_MAX && brun + hb[q] > t) {
-      mine = b0 + q;
-      mine_before = brun;
+    if (brun <= t && brun + hb[q] > t) {
+      fs.ctl[5] = b0 + q;
+      fs.ctlu[0] = brun;
     }
     brun += hb[q];
   }
-  const int b = block_min<int>(mine, fs.redi);
-  if (b == INT_MAX) return V - 1;
-  if (mine == b) fs.ctlu[0] = mine_before;
   if (threadIdx.x == 0) fs.ctl[2] = 0;
-  lds_barrier();
+  __syncthreads();
+  if (btot <= t) return V - 1;
+  const int b = fs.ctl[5];
   const uint64_t before = fs.ctlu[0];
   SortList& sl = fs.u.sl;
-  for (int c = threadIdx.x; c < n; c += kThreads) {
-    const uint64_t w = wt(c);
-    const int idx = cs.idx(c);
-    if (w && ibin(idx) == b) {
-      const int s = lds_fetch_add(&fs.ctl[2], 1);
-      sl.key[s] = (uint64_t)idx;
-      sl.idx[s] = idx;
-      sl.w[s] = w;
+  uint32_t mine = 0;
+#pragma unroll
+  for (int q = 0; q < kPerT; ++q)
+    if (wq(q) && ibin(rc.idx[q]) == b) mine |= 1u << q;
+  int slot = mine ? lds_fetch_add(&fs.ctl[2], __popc(mine)) : 0;
+#pragma unroll
+  for (int q = 0; q < kPerT; ++q)
+    if ((mine >> q) & 1u) {
+      sl.key[slot] = (uint64_t)rc.idx[q];
+      sl.idx[slot] = rc.idx[q];
+      sl.w[slot] = wq(q);
+      ++slot;
     }
-  }
   lds_barrier();
   const int m = fs.ctl[2];  // at most V / kHB + 1 <= kThreads tokens
-  lds_bitonic(sl.key, sl.idx, sl.w, m, ~0ull, [](uint64_t ka, int, uint64_t kb, int) { return ka < kb; });
+  if (m <= kWave) {
+    // one wave: each lane sums the weight of the entries with a smaller
+    // index; the hit is the lane whose weight takes the running mass past t
+    if (wave() == 0) {
+      const int ln = lane();
+      uint64_t w = 0ull;
+      int ix = INT_MAX;
+      if (ln < m) {
+        ix = sl.idx[ln];
+        w = sl.w[ln];
+      }
+      uint64_t ahead = 0;
+#pragma unroll 8
+      for (int j = 0; j < m; ++j)
+        if (sl.idx[j] < ix) ahead += sl.w[j];
+      const bool hit = ln < m && before + ahead <= t && before + ahead + w > t;
+      const uint64_t hbits = __ballot(hit);
+      if (ln == 0 && hbits == 0) fs.ctl[3] = INT_MAX;
+      if (hit) fs.ctl[3] = ix;
+    }
+    lds_barrier();
+    const int hit = fs.ctl[3];
+    return hit == INT_MAX ? V - 1 : hit;
+  }
+  auto idx_asc = [](uint64_t ka, int, uint64_t kb, int) { return ka < kb; };
+  lds_bitonic(sl.key, sl.idx, sl.w, m, ~0ull, idx_asc);
   const uint64_t w = (int)threadIdx.x < m ? sl.w[threadIdx.x] : 0ull;
   uint64_t mt;
   const uint64_t ex = block_excl_scan<uint64_t>(w, fs.redu, &mt);
@@ -679,6 +791,23 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, int row, co
   using G = Geo<TIn>;
   const int V = a.V;
   const int C = a.ws.C, capc = a.ws.capc;
+  // gather every slot of the row first (slot i = q * kThreads + t, chunk
+  // i / capc; consecutive lanes read consecutive addresses), then learn from
+  // the chunk partials which slots hold candidates
+  const int slots = C * capc;
+  const size_t base = (size_t)row * slots;
+  RegCands rc;
+  rc.valid = 0;
+#pragma unroll
+  for (int q = 0; q < kPerT; ++q) {
+    const int i = q * kThreads + (int)threadIdx.x;
+    rc.v[q] = 0.0;
+    rc.idx[q] = 0;
+    if (i < slots) {
+      rc.v[q] = a.ws.cz[base + i];
+      rc.idx[q] = a.ws.ci[base + i];
+    }
+  }
   double u_l = -INFINITY, zm_l = -INFINITY;
   if ((int)threadIdx.x < C) {
     const ChunkPart p = a.ws.part[(size_t)row * C + threadIdx.x];
@@ -688,44 +817,23 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, int row, co
   }
   const double U = block_max(u_l, fs.redd);
   const double zmax = block_max(zm_l, fs.redd);
-  // gather: thread t reads slots [16t, 16t + 16) of the row's C * capc slots
-  constexpr int kPerT = kCandCap / kThreads;
-  const int s0 = kPerT * (int)threadIdx.x;
-  int mine = 0;
-  double zl[kPerT];
-  int il[kPerT];
-  if (s0 < C * capc) {
-    const int c = s0 / capc, l0 = s0 - c * capc;
-    mine = min(max(fs.cnt_c[c] - l0, 0), kPerT);
-    const size_t g = ((size_t)row * C + c) * capc + l0;
 #pragma unroll
-    for (int q = 0; q < kPerT; ++q)
-      if (q < mine) {
-        zl[q] = a.ws.cz[g + q];
-        il[q] = a.ws.ci[g + q];
-      }
-  }
-  uint32_t ntot;
-  const int off = (int)block_excl_scan<uint32_t>((uint32_t)mine, reinterpret_cast<uint32_t*>(fs.redu), &ntot);
-#pragma unroll
-  for (int q = 0; q < kPerT; ++q)
-    if (q < mine) {
-      fs.cz[off + q] = zl[q];
-      fs.ci[off + q] = il[q];
+  for (int q = 0; q < kPerT; ++q) {
+    const int i = q * kThreads + (int)threadIdx.x;
+    if (i < slots) {
+      const int c = i / capc;
+      if (i - c * capc < fs.cnt_c[c]) rc.valid |= 1u << q;
     }
-  __syncthreads();
-  const int n = (int)ntot;
-  const Cands cs{fs.cz, fs.ci};
+  }
   const double T = rp.T;
   auto yexact = [&](double z) -> double { return T == 1.0 ? z : z / T; };
-  const double ymax = yexact(zmax);
-  auto zc = [&](int c) -> double { return fs.cz[c]; };
 
   // ---- top-k: k-th largest with multiplicity, keep y >= kth_y (:76-78)
   double z_lo = -INFINITY;
   if (TOPK) {
-    const SelOut r = cand_select<false>(cs, n, [](int) { return true; }, zc, [&](int c) { return key_of(zc(c)); },
-                                        [](int) { return 0ull; }, (uint64_t)rp.top_k, fs);
+    const SelOut r = cand_select<false>(rc, [](int) { return true; }, [&](int q) { return rc.v[q]; },
+                                        [&](int q) { return key_of(rc.v[q]); }, [](int) { return 0ull; },
+                                        (uint64_t)rp.top_k, fs);
     if (!r.found) return FastOut{V - 1, true};
     const double kth_z = val_of_key(r.key);
     const double kth_y = yexact(kth_z);
@@ -737,16 +845,21 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, int row, co
     }
     if (!(U < z_lo)) return FastOut{V - 1, true};
   }
-  auto elig = [&](int c) -> bool { return zc(c) >= z_lo; };
 
-  // ---- softmax normaliser (:79-81)
+  // ---- softmax (:79-81): each candidate's exp(y - ymax) once, in place of
+  // z (0 outside the top-k set); p = e / S
+  const YScale ys{T, 1.0 / T};
+  const double ymax = ys(zmax);
+  double s = 0.0;
+#pragma unroll
+  for (int q = 0; q < kPerT; ++q) {
+    const double z = rc.v[q];
+    const double e = (((rc.valid >> q) & 1u) && z >= z_lo) ? fast_exp_neg(ys(z) - ymax, fs.exp_tab) : 0.0;
+    rc.v[q] = e;
+    s += e;
+  }
   double S;
   if (TOPK) {
-    double s = 0.0;
-    for (int c = threadIdx.x; c < n; c += kThreads) {
-      const double z = zc(c);
-      if (z >= z_lo) s += fast_exp_neg(yexact(z) - ymax, fs.exp_tab);
-    }
     S = block_sum(s, fs.redd);
   } else {
     const int nseg = (V + G::kSeg - 1) / G::kSeg;
@@ -754,19 +867,19 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, int row, co
     segment_masses(a, row, nseg, fs, &ysmax, &mk, &mass);
     S = block_sum(mass, fs.redd);
   }
-  auto pc = [&](int c) -> double {
-    const double z = zc(c);
-    return z >= z_lo ? fast_exp_neg(yexact(z) - ymax, fs.exp_tab) / S : 0.0;
-  };
+  const double invS = 1.0 / S;
+  auto pq = [&](int q) -> double { return rc.v[q] * invS; };
 
-  // ---- top-p: first token (p desc, index asc) whose inclusive mass reaches top_p (:82-90)
+  // ---- top-p: first token (p desc, index asc) whose inclusive mass reaches
+  // top_p (:82-90); bins on the bit pattern of p (log-spaced)
   bool have_cut = false;
   uint64_t cut_key = 0;
   int cut_idx = INT_MAX;
   if (rp.topp) {
-    const SelOut r = cand_select<true>(cs, n, elig, [&](int c) { return yexact(zc(c)); },
-                                       [&](int c) { return pkey_of(pc(c)); }, [&](int c) { return to_fx(pc(c)); },
-                                       to_fx(rp.top_p), fs);
+    const SelOut r = cand_select<true>(rc, [&](int q) { return rc.v[q] > 0.0; },
+                                       [&](int q) { return (double)pkey_of(pq(q)); },
+                                       [&](int q) { return pkey_of(pq(q)); }, [&](int q) { return to_fx(pq(q)); },
+                                       topp_target(rp.top_p), fs);
     if (r.giveup) return FastOut{V - 1, true};
     if (r.found) {
       have_cut = true;
@@ -774,23 +887,22 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, int row, co
       cut_idx = r.idx;
     }
     if (!TOPK && U > -INFINITY) {
-      const double pU = fast_exp_neg(yexact(U) - ymax, fs.exp_tab) / S;
+      const double pU = fast_exp_neg(ys(U) - ymax, fs.exp_tab) * invS;
       if (!(have_cut && cut_key > pkey_of(pU))) return FastOut{V - 1, true};
     }
   }
 
   // ---- draw in vocabulary order (:94-98)
-  auto wt = [&](int c) -> uint64_t {
-    const double p = pc(c);
+  auto wt = [&](int q) -> uint64_t {
+    const double p = pq(q);
     if (!(p > 0.0)) return 0ull;
     if (have_cut) {
       const uint64_t k = pkey_of(p);
-      const int idx = cs.idx(c);
-      if (!(k > cut_key || (k == cut_key && idx <= cut_idx))) return 0ull;
+      if (!(k > cut_key || (k == cut_key && rc.idx[q] <= cut_idx))) return 0ull;
     }
     return to_fx(p);
   };
-  return FastOut{draw_kept(cs, n, V, rp.u, wt, fs), false};
+  return FastOut{draw_kept(rc, V, rp.u, wt, fs), false};
 }
 
 template <typename TIn, bool VEC>
