@@ -13,6 +13,7 @@
 
 struct plh_ctx {
   int device = 0;
+  int num_cu = 0;
   hipStream_t own_stream = nullptr;
   hipStream_t stream = nullptr;
   unsigned long long* fallback = nullptr;
@@ -109,6 +110,8 @@ int plh_create(plh_ctx** out, int device) {
     if (hipMalloc(&c->fallback, sizeof(unsigned long long)) != hipSuccess) { rc = PLH_ERR_OUT_OF_MEMORY; break; }
     if (hipMemset(c->fallback, 0, sizeof(unsigned long long)) != hipSuccess) { rc = PLH_ERR_HIP; break; }
     if (hipEventCreateWithFlags(&c->ws_done, hipEventDisableTiming) != hipSuccess) { rc = PLH_ERR_HIP; break; }
+    if (hipDeviceGetAttribute(&c->num_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+        c->num_cu <= 0) { rc = PLH_ERR_HIP; break; }
   } while (0);
   if (rc != PLH_OK) {
     plh_destroy(c);
@@ -294,7 +297,7 @@ int plh_sample(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, int
     c->ev_pending.push_back(ev);
     PLH_HIP(c, hipEventRecord(ev[0], c->stream), "hipEventRecord");
   }
-  const hipError_t e = plh::launch_sample_fast(a, f64, vec, c->stream, ev[1]);
+  const hipError_t e = plh::launch_sample_fast(a, f64, vec, c->num_cu, c->stream, ev[1]);
   if (e != hipSuccess) return hip_fail(c, e, "plh_sample launch");
   if (c->timing) PLH_HIP(c, hipEventRecord(ev[2], c->stream), "hipEventRecord");
   PLH_HIP(c, hipEventRecord(c->ws_done, c->stream), "hipEventRecord");

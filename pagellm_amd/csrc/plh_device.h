@@ -30,6 +30,15 @@ constexpr int kWaves = kThreads / kWave;
 constexpr double kFxScale = 4611686018427387904.0;
 
 __device__ __forceinline__ int lane() { return threadIdx.x & (kWave - 1); }
+
+// Workgroup barrier for LDS communication: the calling wave's LDS operations
+// complete, then s_barrier.  Unlike __syncthreads() it carries no
+// memory-model fence, so vector-memory loads in flight (into registers, or
+// global->LDS loads into another buffer) stay in flight across it; the
+// "memory" clobber keeps the compiler from moving memory accesses over it.
+// Every barrier in this library orders LDS traffic only: no thread reads
+// global memory written by another thread of its workgroup.
+__device__ __forceinline__ void wg_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __device__ __forceinline__ int wave() { return threadIdx.x >> 6; }
 
 // Larger double -> larger key; -0.0 and +0.0 share a key (numpy compares them
@@ -95,6 +104,9 @@ __device__ __forceinline__ void lds_or(uint32_t* p, uint32_t v) {
 __device__ __forceinline__ void lds_min(int* p, int v) {
   __hip_atomic_fetch_min(PLH_LDS(int, p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
+__device__ __forceinline__ void lds_max(int* p, int v) {
+  __hip_atomic_fetch_max(PLH_LDS(int, p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
 
 // Device-wide counters in global memory (address space 1), agent scope.
 #define PLH_GLB(T, p) ((__attribute__((address_space(1))) T*)(p))
@@ -127,6 +139,20 @@ __device__ __forceinline__ T dpp(T old, T src) {
                                                               ROWM, 0xf, false);
     return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
   }
+}
+
+// A value the caller knows to be the same in every lane (a workgroup
+// reduction read back from LDS, say), moved to scalar registers so that it
+// costs no VGPRs.
+__device__ __forceinline__ double uniform(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32));
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ uint64_t uniform(uint64_t v) {
+  return __builtin_bit_cast(uint64_t, uniform(__builtin_bit_cast(double, v)));
 }
 
 // Value of lane l (uniform).
@@ -194,11 +220,11 @@ template <typename T>
 __device__ __forceinline__ T block_sum(T v, T* red) {
   v = wave_sum(v);
   if (lane() == 0) red[wave()] = v;
-  __syncthreads();
+  wg_barrier();
   T r = red[0];
 #pragma unroll
   for (int w = 1; w < kWaves; ++w) r += red[w];
-  __syncthreads();
+  wg_barrier();
   return r;
 }
 
@@ -206,11 +232,11 @@ template <typename T>
 __device__ __forceinline__ T block_max(T v, T* red) {
   v = wave_max(v);
   if (lane() == 0) red[wave()] = v;
-  __syncthreads();
+  wg_barrier();
   T r = red[0];
 #pragma unroll
   for (int w = 1; w < kWaves; ++w) r = red[w] > r ? red[w] : r;
-  __syncthreads();
+  wg_barrier();
   return r;
 }
 
@@ -218,11 +244,11 @@ template <typename T>
 __device__ __forceinline__ T block_min(T v, T* red) {
   v = wave_min(v);
   if (lane() == 0) red[wave()] = v;
-  __syncthreads();
+  wg_barrier();
   T r = red[0];
 #pragma unroll
   for (int w = 1; w < kWaves; ++w) r = red[w] < r ? red[w] : r;
-  __syncthreads();
+  wg_barrier();
   return r;
 }
 
@@ -234,6 +260,19 @@ struct ArgMax {
 
 __device__ __forceinline__ ArgMax argmax_merge(ArgMax a, ArgMax b) {
   return (b.v > a.v || (b.v == a.v && b.i < a.i)) ? b : a;
+}
+
+// Wave argmax (value, lowest index); every lane receives the result.
+__device__ __forceinline__ ArgMax wave_argmax(ArgMax a) {
+  const ArgMax id{-INFINITY, INT_MAX};
+  auto step = [&](ArgMax o) { a = argmax_merge(a, o); };
+  step(ArgMax{dpp<kDppRowShr1, 0xf>(id.v, a.v), dpp<kDppRowShr1, 0xf>(id.i, a.i)});
+  step(ArgMax{dpp<kDppRowShr2, 0xf>(id.v, a.v), dpp<kDppRowShr2, 0xf>(id.i, a.i)});
+  step(ArgMax{dpp<kDppRowShr4, 0xf>(id.v, a.v), dpp<kDppRowShr4, 0xf>(id.i, a.i)});
+  step(ArgMax{dpp<kDppRowShr8, 0xf>(id.v, a.v), dpp<kDppRowShr8, 0xf>(id.i, a.i)});
+  step(ArgMax{dpp<kDppRowBcast15, 0xa>(id.v, a.v), dpp<kDppRowBcast15, 0xa>(id.i, a.i)});
+  step(ArgMax{dpp<kDppRowBcast31, 0xc>(id.v, a.v), dpp<kDppRowBcast31, 0xc>(id.i, a.i)});
+  return ArgMax{lane_value(a.v, kWave - 1), lane_value(a.i, kWave - 1)};
 }
 
 __device__ __forceinline__ ArgMax block_argmax(ArgMax a, double* redd, int* redi) {
@@ -250,11 +289,11 @@ __device__ __forceinline__ ArgMax block_argmax(ArgMax a, double* redd, int* redi
     redd[wave()] = a.v;
     redi[wave()] = a.i;
   }
-  __syncthreads();
+  wg_barrier();
   ArgMax r{redd[0], redi[0]};
 #pragma unroll
   for (int w = 1; w < kWaves; ++w) r = argmax_merge(r, ArgMax{redd[w], redi[w]});
-  __syncthreads();
+  wg_barrier();
   return r;
 }
 
@@ -264,7 +303,7 @@ template <typename T>
 __device__ __forceinline__ T block_excl_scan(T v, T* red, T* total) {
   const T x = wave_scan_incl(v, T(0), OpAdd{});
   if (lane() == kWave - 1) red[wave()] = x;
-  __syncthreads();
+  wg_barrier();
   T pre = 0, tot = 0;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
@@ -272,7 +311,7 @@ __device__ __forceinline__ T block_excl_scan(T v, T* red, T* total) {
     if (w < wave()) pre += s;
     tot += s;
   }
-  __syncthreads();
+  wg_barrier();
   *total = tot;
   return pre + (x - v);
 }

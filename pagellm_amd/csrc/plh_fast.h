@@ -23,8 +23,16 @@ __device__ __forceinline__ void init_exp_table(double* tab) {
   if (threadIdx.x < 64) tab[threadIdx.x] = exp2((double)threadIdx.x / 64.0);
 }
 
+// The calling wave's own copy (needs no workgroup barrier before use: a
+// wave's LDS accesses complete in order).
+__device__ __forceinline__ void init_exp_table_wave(double* tab) {
+  tab[lane()] = exp2((double)lane() / 64.0);
+}
+
 __device__ __forceinline__ double fast_exp_neg(double d, const double* tab) {
-  if (!(d > -745.2)) return 0.0;  // also -inf
+  // below -745.2 the result underflows: clamping to -1000 keeps k*ln2/64
+  // exact and makes the final ldexp return 0 (also for -inf)
+  d = fmax(d, -1000.0);
   const double kd = __builtin_rint(d * (64.0 / 0.6931471805599453));
   const int k = (int)kd;
   double r = fma(-kd, kLn2Hi / 64.0, d);
@@ -75,7 +83,7 @@ __device__ __forceinline__ void lds_bitonic(uint64_t* key, int* idx, uint64_t* w
       idx[i] = INT_MAX;
       w[i] = 0ull;
     }
-  __syncthreads();
+  wg_barrier();
   for (int k = 2; k <= N; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
       for (int i = threadIdx.x; i < N; i += kThreads) {
@@ -95,7 +103,7 @@ __device__ __forceinline__ void lds_bitonic(uint64_t* key, int* idx, uint64_t* w
           }
         }
       }
-      __syncthreads();
+      wg_barrier();
     }
   }
 }
@@ -141,9 +149,9 @@ __device__ __forceinline__ Pick pick_desc(const uint32_t* cnt, const uint64_t* m
       run += v[j];
     }
   }
-  __syncthreads();
+  wg_barrier();
   const Pick p{true, ctl[0], ctlu[1]};
-  __syncthreads();
+  wg_barrier();
   return p;
 }
 

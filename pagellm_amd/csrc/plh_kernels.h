@@ -7,18 +7,22 @@
 
 namespace plh {
 
-// Per-chunk partial left by k_sample_chunks for k_sample_final.
-struct ChunkPart {
-  double zmax;   // largest finite penalised logit of the chunk (-inf if none)
-  double umax;   // largest finite one not kept as a candidate (-inf if none)
-  double best_z; // greedy rows: the chunk's argmax value ...
-  int best_idx;  // ... and its token id
-  int n;         // candidates written (at most capc)
+// Partial left by one wave of k_sample_chunks (its segment, 1/8 of a
+// chunk) for k_sample_final.
+struct WavePart {
+  double zmax;    // largest finite penalised logit of the segment (-inf if none)
+  double umax;    // largest finite one not kept as a candidate (-inf if none)
+  double best_z;  // greedy rows: the segment's argmax value ...
+  int best_idx;   // ... and its token id
+  int end;        // candidate rows: end of the wave's slots in its chunk's list
+                  // (the chunk's candidate count is the largest end)
+  int flags;      // kChunkIncomplete: the row needs the general pipeline
 };
+constexpr int kChunkIncomplete = 1;
 
 // Workspace of the two-launch fast path, carved from one device buffer.
 struct ChunkWs {
-  ChunkPart* part;  // [B * C]
+  WavePart* part;   // [B * C * 8], entry (chunk * 8 + wave)
   double* seg_m;    // [B * C * 8] per-wave segment max of z / T
   double* seg_s;    // [B * C * 8] per-wave segment sum of exp(z / T - max)
   double* cz;       // [B * C * capc] candidate penalised logits
@@ -80,8 +84,9 @@ hipError_t launch_sample_rows(const SampleArgs& a, bool f64, bool vec, hipStream
 // (256-byte aligned), and the two launches.
 size_t fast_ws_bytes(int B, int V, bool f64);
 ChunkWs fast_ws_layout(void* base, int B, int V, bool f64);
-// `between`, when not null, is recorded on s between the two kernels.
-hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, hipStream_t s,
+// Aligned rows (vec) stream through num_cu persistent workgroups; `between`,
+// when not null, is recorded on s between the two kernels.
+hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, int num_cu, hipStream_t s,
                               hipEvent_t between = nullptr);
 hipError_t launch_draw(const DrawArgs& a, bool f64, hipStream_t s);
 hipError_t launch_penalize(const PenalizeArgs& a, bool f64, hipStream_t s);

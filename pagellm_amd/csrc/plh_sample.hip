@@ -85,13 +85,8 @@ union SmemAll {
   Smem g;
 };
 
-// Workgroup barrier ordering LDS only: global loads issued ahead of it stay
-// in flight.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
+// Workgroup barrier ordering LDS only (wg_barrier).
+__device__ __forceinline__ void lds_barrier() { wg_barrier(); }
 
 __device__ __forceinline__ RowParams load_row_params(const SampleArgs& a, int row) {
   RowParams rp;
@@ -151,15 +146,23 @@ struct VecOf<double> {
   typedef d2_t T;
 };
 
+// Penalised tokens a wave keeps aside (their exact float64 value); a wave
+// with more makes its chunk incomplete (the row takes the general
+// pipeline).
+constexpr int kPenPerWave = 128;
+
+// LDS of k_sample_chunks: about 23 KB.
 struct ChunkSmem {
   double redd[2 * kWaves];
   uint64_t redu[kWaves];
   int redi[kWaves];
   int ctl[8];
   uint64_t ctlu[4];
-  double exp_tab[64];
+  double exp_tab[kWaves][64];  // one copy per wave
   uint32_t hcnt[kHB];
   uint32_t bitmap[Geo<float>::kChunk / 32];
+  double pz[kWaves][kPenPerWave];
+  int pt[kWaves][kPenPerWave];
   int cand_n;
 };
 
@@ -220,7 +223,7 @@ __device__ __forceinline__ void block_minmax(double* lo, double* hi, double* red
     red[wave()] = a;
     red[kWaves + wave()] = b;
   }
-  __syncthreads();
+  wg_barrier();
   a = red[0];
   b = red[kWaves];
 #pragma unroll
@@ -228,135 +231,252 @@ __device__ __forceinline__ void block_minmax(double* lo, double* hi, double* red
     a = fmin(a, red[w]);
     b = fmax(b, red[kWaves + w]);
   }
-  __syncthreads();
+  wg_barrier();
   *lo = a;
   *hi = b;
 }
 
-// Candidates of one chunk: every finite z >= theta, where theta is the
-// lower edge of the value-histogram bin that holds the target-th largest
-// (all finite tokens when there are fewer).  Writes them to the chunk's
-// workspace slots; the largest finite z not written goes to part->umax.
+// The calling thread's tokens of one chunk: the raw registers (penalised
+// slots hold -inf) plus its penalised tokens kept aside in its wave's LDS
+// pool, entries [po, po + np), with their exact float64 value.  Every pass
+// below visits both.
 template <typename TIn>
-__device__ __forceinline__ void chunk_candidates(const double (&z)[Geo<TIn>::kEpt], const SampleArgs& a,
-                                                 const RowParams& rp, int c0, ChunkSmem& cm) {
+struct ChunkToks {
+  using G = Geo<TIn>;
+  typename VecOf<TIn>::T v[kU];
+  int po = 0, np = 0;
+  __device__ __forceinline__ double raw(int e) const { return (double)v[e / G::kVW][e % G::kVW]; }
+  // Called at the start of each pass: the compiler must then widen the
+  // registers again instead of keeping a float64 copy of the chunk alive
+  // across passes (64 more VGPRs, which would cost occupancy).
+  __device__ __forceinline__ void new_pass() {
+#pragma unroll
+    for (int j = 0; j < kU; ++j) asm volatile("" : "+v"(v[j]));
+  }
+  __device__ __forceinline__ double pen_z(const ChunkSmem& cm, int i) const { return cm.pz[wave()][po + i]; }
+  __device__ __forceinline__ int pen_tok(const ChunkSmem& cm, int i) const { return cm.pt[wave()][po + i]; }
+};
+
+// Moves the calling wave's penalised tokens (bits pb of each lane) out of
+// the registers: their penalised float64 value goes to the wave's LDS pool,
+// the register slot to -inf.  Returns true when the pool overflows (the
+// chunk is then incomplete).
+template <typename TIn>
+__device__ __forceinline__ bool set_aside_penalised(ChunkToks<TIn>& tk, uint32_t pb, double pen, int c0, ChunkSmem& cm) {
+  using G = Geo<TIn>;
+  const int n = __popc(pb);
+  const int incl = wave_scan_incl(n, 0, OpAdd{});
+  const int total = lane_value(incl, kWave - 1);
+  tk.po = incl - n;
+  tk.np = 0;
+  if (total > kPenPerWave) return true;
+  tk.np = n;
+  if (pb != 0u) {
+    int k = tk.po;
+#pragma unroll
+    for (int e = 0; e < G::kEpt; ++e) {
+      if ((pb >> e) & 1u) {
+        cm.pz[wave()][k] = penalize(tk.raw(e), pen);
+        cm.pt[wave()][k] = c0 + slot_q<TIn>(e);
+        ++k;
+        tk.v[e / G::kVW][e % G::kVW] = (TIn)(-INFINITY);
+      }
+    }
+  }
+  return false;
+}
+
+// Candidates of one chunk: every finite z >= theta, with theta below the
+// chunk's target-th largest token (all finite tokens when there are fewer).
+//   top-k, k <= 512: the k-th largest of the workgroup's 512 per-thread
+//     maxima is itself k tokens deep, so a histogram of those maxima alone
+//     bounds the k-th largest token from below;
+//   otherwise: a value histogram of all the chunk's tokens.
+// theta is the lower edge of the histogram bin holding the target-th
+// largest (cm.hcnt is zeroed at kernel start).  Each wave writes its
+// candidates to a range of the chunk's slots and its part: the chunk's
+// largest z, the largest finite z of its segment not written, the end of
+// its slots.  lmax is the calling thread's largest z.
+template <typename TIn>
+__device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax, const SampleArgs& a,
+                                                 const RowParams& rp, int g, int c0, int flags, WavePart* wp,
+                                                 ChunkSmem& cm) {
   constexpr int kEpt = Geo<TIn>::kEpt;
   const int capc = a.ws.capc;
   // top-p rows keep as many as the slots allow, less a margin for the
   // histogram bin that straddles the threshold
   const uint64_t keep = (uint64_t)(capc - capc / 16);
   const uint64_t target = rp.topk ? min((uint64_t)rp.top_k, keep) : keep;
-  double lo = INFINITY, hi = -INFINITY;
+  const bool by_max = rp.topk && target <= (uint64_t)kThreads;
+  double lo = INFINITY, hi = lmax;
+  if (by_max) {
+    if (lmax > -INFINITY) lo = lmax;
+  } else {
+    tk.new_pass();
 #pragma unroll
-  for (int e = 0; e < kEpt; ++e)
-    if (z[e] > -INFINITY) {
-      lo = fmin(lo, z[e]);
-      hi = fmax(hi, z[e]);
+    for (int e = 0; e < kEpt; ++e) {
+      const double z = tk.raw(e);
+      if (z > -INFINITY) lo = fmin(lo, z);
     }
+    for (int i = 0; i < tk.np; ++i) {
+      const double z = tk.pen_z(cm, i);
+      if (z > -INFINITY) lo = fmin(lo, z);
+    }
+  }
   block_minmax(&lo, &hi, cm.redd);
+  lo = uniform(lo);
+  hi = uniform(hi);
   double theta = -INFINITY;
   if (hi > -INFINITY) {
     const Affine af = make_affine(lo, hi, kHB);
-    for (int b = threadIdx.x; b < kHB; b += kThreads) cm.hcnt[b] = 0u;
-    lds_barrier();
+    if (by_max) {
+      if (lmax > -INFINITY) lds_add(&cm.hcnt[af.bin(lmax)], 1u);
+    } else {
+      tk.new_pass();
 #pragma unroll
-    for (int e = 0; e < kEpt; ++e)
-      if (z[e] > -INFINITY) lds_add(&cm.hcnt[af.bin(z[e])], 1u);
+      for (int e = 0; e < kEpt; ++e) {
+        const double z = tk.raw(e);
+        if (z > -INFINITY) lds_add(&cm.hcnt[af.bin(z)], 1u);
+      }
+      for (int i = 0; i < tk.np; ++i) {
+        const double z = tk.pen_z(cm, i);
+        if (z > -INFINITY) lds_add(&cm.hcnt[af.bin(z)], 1u);
+      }
+    }
     lds_barrier();
     const Pick pk = pick_desc<false>(cm.hcnt, nullptr, kHB, 0, target, cm.redu, cm.ctl, cm.ctlu);
     // every z with bin(z) >= d is >= lo + (d - 0.01) / scale (bin(z) is
-    // floor((z - lo) * scale) up to a few ulps)
-    if (pk.found && pk.d > 0) theta = af.lo + ((double)pk.d - 0.01) / af.scale;
+    // floor((z - lo) * scale) up to a few ulps); bin 0 starts at lo
+    if (pk.found) theta = pk.d > 0 ? af.lo + ((double)uniform(pk.d) - 0.01) / af.scale : lo;
   }
+  theta = uniform(theta);
   uint32_t pm = 0;
   double um = -INFINITY;
+  tk.new_pass();
 #pragma unroll
   for (int e = 0; e < kEpt; ++e) {
-    const bool fin = z[e] > -INFINITY;
-    if (fin && z[e] >= theta) pm |= 1u << e;
-    else if (fin) um = fmax(um, z[e]);
+    const double z = tk.raw(e);
+    const bool fin = z > -INFINITY;
+    if (fin && z >= theta) pm |= 1u << e;
+    else if (fin) um = fmax(um, z);
   }
-  // one LDS reservation per wave
-  const int cnt = __popc(pm);
+  uint32_t qm = 0;  // penalised tokens kept
+  for (int i = 0; i < tk.np; ++i) {
+    const double z = tk.pen_z(cm, i);
+    const bool fin = z > -INFINITY;
+    if (fin && z >= theta) qm |= 1u << i;
+    else if (fin) um = fmax(um, z);
+  }
+  // one LDS reservation per wave (cm.cand_n was reset before the barriers above)
+  const int cnt = __popc(pm) + __popc(qm);
   const int incl = wave_scan_incl(cnt, 0, OpAdd{});
+  const int wtot = lane_value(incl, kWave - 1);
   int base = 0;
   if (lane() == kWave - 1) base = lds_fetch_add(&cm.cand_n, incl);
   base = lane_value(base, kWave - 1);
   int slot = base + incl - cnt;
-  double* cz = a.ws.cz + (size_t)blockIdx.x * capc;
-  int32_t* ci = a.ws.ci + (size_t)blockIdx.x * capc;
+  double* cz = a.ws.cz + (size_t)g * capc;
+  int32_t* ci = a.ws.ci + (size_t)g * capc;
+  tk.new_pass();
 #pragma unroll
   for (int e = 0; e < kEpt; ++e) {
     if ((pm >> e) & 1u) {
       if (slot < capc) {
-        cz[slot] = z[e];
+        cz[slot] = tk.raw(e);
         ci[slot] = c0 + slot_q<TIn>(e);
       } else {
-        um = fmax(um, z[e]);
+        um = fmax(um, tk.raw(e));
       }
       ++slot;
     }
   }
-  um = block_max(um, cm.redd);
-  if (threadIdx.x == 0) {
-    ChunkPart* part = a.ws.part + blockIdx.x;
-    part->zmax = hi;
-    part->umax = um;
-    part->n = min(cm.cand_n, capc);
+  for (int i = 0; i < tk.np; ++i) {
+    if ((qm >> i) & 1u) {
+      if (slot < capc) {
+        cz[slot] = tk.pen_z(cm, i);
+        ci[slot] = tk.pen_tok(cm, i);
+      } else {
+        um = fmax(um, tk.pen_z(cm, i));
+      }
+      ++slot;
+    }
+  }
+  um = wave_max(um);
+  if (lane() == 0) {
+    wp->zmax = hi;
+    wp->umax = um;
+    wp->end = min(base + wtot, capc);
+    wp->flags = flags;
   }
 }
 
+// One workgroup per 64 KB chunk (rows of any alignment: 16-byte
+// non-temporal loads when the row allows, scalar loads otherwise).  The
+// waves work on their own segments and write their own parts, so greedy and
+// temperature chunks need no workgroup barrier; candidate chunks need the
+// few of one value histogram.  Per row mode: greedy argmax, candidates,
+// segment partials of the normaliser.
 template <typename TIn, bool VEC>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_sample_chunks(SampleArgs a) {
   using G = Geo<TIn>;
   __shared__ ChunkSmem cm;
   const int C = a.ws.C;
-  const int row = blockIdx.x / C;
-  const int c0 = (blockIdx.x - row * C) * G::kChunk;
+  const int g = blockIdx.x;
+  const int row = g / C;
+  const int c0 = (g - row * C) * G::kChunk;
   const RowParams rp = load_row_params(a, row);
   const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
-  typename VecOf<TIn>::T v[kU];
-  load_chunk<TIn, VEC>(x, a.V, c0, v);
-  init_exp_table(cm.exp_tab);
-  if (threadIdx.x == 0) cm.cand_n = 0;
-  const uint32_t pb = rp.pen_active ? chunk_pbits<TIn>(a, rp, c0, cm) : 0u;
-  lds_barrier();
-  double z[G::kEpt];
-#pragma unroll
-  for (int e = 0; e < G::kEpt; ++e) z[e] = (double)v[e / G::kVW][e % G::kVW];
-  if (pb != 0u) {
-#pragma unroll
-    for (int e = 0; e < G::kEpt; ++e)
-      if ((pb >> e) & 1u) z[e] = penalize(z[e], rp.pen);
+  ChunkToks<TIn> tk;
+  load_chunk<TIn, VEC>(x, a.V, c0, tk.v);
+  const double* tab = cm.exp_tab[wave()];
+  init_exp_table_wave(cm.exp_tab[wave()]);
+  const bool cands = rp.topk || rp.topp;
+  if (cands) {  // ordered before use by the first barrier of chunk_candidates
+    for (int b = threadIdx.x; b < kHB; b += kThreads) cm.hcnt[b] = 0u;
+    if (threadIdx.x == 0) cm.cand_n = 0;
   }
+  int flags = 0;
+  if (rp.pen_active) {
+    const uint32_t pb = chunk_pbits<TIn>(a, rp, c0, cm);
+    if (set_aside_penalised<TIn>(tk, pb, rp.pen, c0, cm)) flags = kChunkIncomplete;
+  }
+  WavePart* wp = a.ws.part + (size_t)g * kWaves + wave();
   if (rp.greedy) {
     ArgMax best{-INFINITY, INT_MAX};
+    tk.new_pass();
 #pragma unroll
-    for (int e = 0; e < G::kEpt; ++e) best = argmax_merge(best, ArgMax{z[e], c0 + slot_q<TIn>(e)});
-    best = block_argmax(best, cm.redd, cm.redi);
-    if (threadIdx.x == 0) {
-      a.ws.part[blockIdx.x].best_z = best.v;
-      a.ws.part[blockIdx.x].best_idx = best.i;
+    for (int e = 0; e < G::kEpt; ++e) best = argmax_merge(best, ArgMax{tk.raw(e), c0 + slot_q<TIn>(e)});
+    for (int i = 0; i < tk.np; ++i) best = argmax_merge(best, ArgMax{tk.pen_z(cm, i), tk.pen_tok(cm, i)});
+    best = wave_argmax(best);
+    if (lane() == 0) {
+      wp->best_z = best.v;
+      wp->best_idx = best.i;
+      wp->flags = flags;
     }
     return;
   }
-  // candidates first: the segment pass below is then the last use of z
-  if (rp.topk || rp.topp) chunk_candidates<TIn>(z, a, rp, c0, cm);
-  if (!rp.topk) {  // the full-vocabulary normaliser (sampling.py:79-81)
-    const YScale ys{rp.T, 1.0 / rp.T};
-    double m = -INFINITY;
+  double lmax = -INFINITY;
+  tk.new_pass();
 #pragma unroll
-    for (int e = 0; e < G::kEpt; ++e) m = fmax(m, ys(z[e]));
-    m = wave_max(m);
+  for (int e = 0; e < G::kEpt; ++e) lmax = fmax(lmax, tk.raw(e));
+  for (int i = 0; i < tk.np; ++i) lmax = fmax(lmax, tk.pen_z(cm, i));
+  if (cands) chunk_candidates<TIn>(tk, lmax, a, rp, g, c0, flags, wp, cm);
+  else if (lane() == 0) wp->flags = flags;
+  if (!rp.topk) {  // the full-vocabulary normaliser (sampling.py:79-81)
+    // y = z / T is monotone in z, so the segment's max y is y(max z)
+    const YScale ys{rp.T, 1.0 / rp.T};
+    const double m = uniform(ys(wave_max(lmax)));
     double s = 0.0;
     if (m > -INFINITY) {
+      tk.new_pass();
 #pragma unroll
-      for (int e = 0; e < G::kEpt; ++e) s += fast_exp_neg(ys(z[e]) - m, cm.exp_tab);
+      for (int e = 0; e < G::kEpt; ++e) s += fast_exp_neg(ys(tk.raw(e)) - m, tab);
+      for (int i = 0; i < tk.np; ++i) s += fast_exp_neg(ys(tk.pen_z(cm, i)) - m, tab);
     }
     s = wave_sum(s);
     if (lane() == 0) {
-      a.ws.seg_m[(size_t)blockIdx.x * kWaves + wave()] = m;
-      a.ws.seg_s[(size_t)blockIdx.x * kWaves + wave()] = s;
+      a.ws.seg_m[(size_t)g * kWaves + wave()] = m;
+      a.ws.seg_s[(size_t)g * kWaves + wave()] = s;
     }
   }
 }
@@ -369,13 +489,13 @@ __device__ __forceinline__ double block_scan_d(double v, double* red, double* ex
   const double x = wave_scan_incl(v, 0.0, OpAdd{});
   const double xe = wave_shift_up1(x, 0.0);
   if (lane() == kWave - 1) red[wave()] = x;
-  __syncthreads();
+  wg_barrier();
   double pre = 0.0, tot = 0.0;
   for (int w = 0; w < kWaves; ++w) {
     if (w < wave()) pre += red[w];
     tot += red[w];
   }
-  __syncthreads();
+  wg_barrier();
   *excl = pre + xe;
   *total = tot;
   return pre + x;
@@ -418,7 +538,7 @@ __device__ __forceinline__ void block_range(double* lo, double* hi, uint32_t* cn
     fs.redm[kWaves + wave()] = b;
     reinterpret_cast<uint32_t*>(fs.redu)[wave()] = n;
   }
-  __syncthreads();
+  wg_barrier();
   a = fs.redm[0];
   b = fs.redm[kWaves];
   n = reinterpret_cast<uint32_t*>(fs.redu)[0];
@@ -428,7 +548,7 @@ __device__ __forceinline__ void block_range(double* lo, double* hi, uint32_t* cn
     b = fmax(b, fs.redm[kWaves + w]);
     n += reinterpret_cast<uint32_t*>(fs.redu)[w];
   }
-  __syncthreads();
+  wg_barrier();
   *lo = a;
   *hi = b;
   *cnt = n;
@@ -636,7 +756,7 @@ __device__ __forceinline__ int draw_kept(const RegCands& rc, int V, double u, co
     brun += hb[q];
   }
   if (threadIdx.x == 0) fs.ctl[2] = 0;
-  __syncthreads();
+  wg_barrier();
   if (btot <= t) return V - 1;
   const int b = fs.ctl[5];
   const uint64_t before = fs.ctlu[0];
@@ -690,12 +810,12 @@ __device__ __forceinline__ int draw_kept(const RegCands& rc, int V, double u, co
   return hit == INT_MAX ? V - 1 : hit;
 }
 
-// Greedy rows: argmax over the chunk argmaxes (lowest index on ties).
+// Greedy rows: argmax over the segment argmaxes (lowest index on ties).
 __device__ __forceinline__ int finish_greedy(const SampleArgs& a, int row, FastSmem& fs) {
-  const int C = a.ws.C;
+  const int P = a.ws.C * kWaves;
   ArgMax best{-INFINITY, INT_MAX};
-  for (int c = threadIdx.x; c < C; c += kThreads) {
-    const ChunkPart& p = a.ws.part[(size_t)row * C + c];
+  for (int c = threadIdx.x; c < P; c += kThreads) {
+    const WavePart& p = a.ws.part[(size_t)row * P + c];
     best = argmax_merge(best, ArgMax{p.best_z, p.best_idx});
   }
   return block_argmax(best, fs.redd, fs.redi).i;
@@ -738,13 +858,13 @@ __device__ __forceinline__ int finish_temp(const SampleArgs& a, int row, const R
   const int s0 = kstar * G::kSeg;
   if (rp.pen_active) {
     for (int w = threadIdx.x; w < G::kSeg / 32; w += kThreads) fs.u.segbits[w] = 0u;
-    __syncthreads();
+    wg_barrier();
     for (int64_t h = rp.h0 + threadIdx.x; h < rp.h1; h += kThreads) {
       const int off = a.hist_ids[h] - s0;
       if ((unsigned)off < (unsigned)G::kSeg) lds_or(&fs.u.segbits[off >> 5], 1u << (off & 31));
     }
   }
-  __syncthreads();
+  wg_barrier();
   const double before = __longlong_as_double((long long)fs.ctlu[0]);
   const double ms = __longlong_as_double((long long)fs.ctlu[1]);
   const double sc = fast_exp_neg(ms - ymax, fs.exp_tab);
@@ -808,10 +928,13 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, int row, co
       rc.idx[q] = a.ws.ci[base + i];
     }
   }
+  // a chunk's candidate count is the largest end over its waves
+  if ((int)threadIdx.x < C) fs.cnt_c[threadIdx.x] = 0;
+  wg_barrier();
   double u_l = -INFINITY, zm_l = -INFINITY;
-  if ((int)threadIdx.x < C) {
-    const ChunkPart p = a.ws.part[(size_t)row * C + threadIdx.x];
-    fs.cnt_c[threadIdx.x] = p.n;
+  if ((int)threadIdx.x < C * kWaves) {
+    const WavePart p = a.ws.part[(size_t)row * C * kWaves + threadIdx.x];
+    lds_max(&fs.cnt_c[threadIdx.x / kWaves], p.end);
     u_l = p.umax;
     zm_l = p.zmax;
   }
@@ -912,10 +1035,15 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   const int row = blockIdx.x;
   const RowParams rp = load_row_params(a, row);
   init_exp_table(fs.exp_tab);
-  __syncthreads();
-  int id;
-  bool general = false;
-  if (rp.greedy) {
+  wg_barrier();
+  int id = 0;
+  // a chunk that could not keep all its penalised tokens aside sends the
+  // row to the general pipeline
+  int fl = 0;
+  for (int c = threadIdx.x; c < a.ws.C * kWaves; c += kThreads) fl |= a.ws.part[(size_t)row * a.ws.C * kWaves + c].flags;
+  bool general = block_max<int>(fl, fs.redi) != 0;
+  if (general) {
+  } else if (rp.greedy) {
     id = finish_greedy(a, row, fs);
   } else if (!rp.topk && !rp.topp) {
     id = finish_temp<TIn>(a, row, rp, fs);
@@ -925,7 +1053,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
     general = o.general;
   }
   if (general) {
-    __syncthreads();
+    wg_barrier();
     if (threadIdx.x == 0) glb_add(a.fallback_rows, 1ull);
     id = row_general<TIn, VEC>(a, row, rp, sm.g, nullptr);
   }
@@ -964,7 +1092,7 @@ __global__ __launch_bounds__(kThreads) void k_penalize(PenalizeArgs a) {
   const int64_t h0 = a.hist_off != nullptr ? a.hist_off[row] : 0;
   const int64_t h1 = a.hist_off != nullptr ? a.hist_off[row + 1] : 0;
   if (pen == 1.0 || h1 <= h0 || a.hist_ids == nullptr) return;
-  __syncthreads();
+  wg_barrier();
   const TIn pn = (TIn)pen;
   for (int64_t h = h0 + threadIdx.x; h < h1; h += kThreads) {
     const int id = a.hist_ids[h];
@@ -997,7 +1125,7 @@ size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 size_t fast_ws_bytes(int B, int V, bool f64) {
   const size_t C = (size_t)chunks_of(V, f64), cap = (size_t)capc_of((int)C), n = (size_t)B * C;
-  return up256(n * sizeof(ChunkPart)) + 2 * up256(n * kWaves * sizeof(double)) + up256(n * cap * sizeof(double)) +
+  return up256(n * kWaves * sizeof(WavePart)) + 2 * up256(n * kWaves * sizeof(double)) + up256(n * cap * sizeof(double)) +
          up256(n * cap * sizeof(int32_t));
 }
 
@@ -1007,8 +1135,8 @@ ChunkWs fast_ws_layout(void* base, int B, int V, bool f64) {
   w.capc = capc_of(w.C);
   const size_t n = (size_t)B * w.C;
   char* p = static_cast<char*>(base);
-  w.part = reinterpret_cast<ChunkPart*>(p);
-  p += up256(n * sizeof(ChunkPart));
+  w.part = reinterpret_cast<WavePart*>(p);
+  p += up256(n * kWaves * sizeof(WavePart));
   w.seg_m = reinterpret_cast<double*>(p);
   p += up256(n * kWaves * sizeof(double));
   w.seg_s = reinterpret_cast<double*>(p);
@@ -1031,17 +1159,23 @@ hipError_t launch_sample_rows(const SampleArgs& a, bool f64, bool vec, hipStream
   return hipGetLastError();
 }
 
-hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, hipStream_t s, hipEvent_t between) {
-  const dim3 gc((unsigned)a.B * (unsigned)a.ws.C), gf(a.B), block(kThreads);
-  auto chunks = f64 ? (vec ? k_sample_chunks<double, true> : k_sample_chunks<double, false>)
-                    : (vec ? k_sample_chunks<float, true> : k_sample_chunks<float, false>);
-  auto final_ = f64 ? (vec ? k_sample_final<double, true> : k_sample_final<double, false>)
-                    : (vec ? k_sample_final<float, true> : k_sample_final<float, false>);
-  hipLaunchKernelGGL(chunks, gc, block, 0, s, a);
+hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, int num_cu, hipStream_t s, hipEvent_t between) {
+  (void)num_cu;
+  const int total = a.B * a.ws.C;
+  const dim3 gf(a.B), block(kThreads);
+  if (vec) {
+    if (f64) hipLaunchKernelGGL((k_sample_chunks<double, true>), dim3(total), block, 0, s, a);
+    else hipLaunchKernelGGL((k_sample_chunks<float, true>), dim3(total), block, 0, s, a);
+  } else {
+    if (f64) hipLaunchKernelGGL((k_sample_chunks<double, false>), dim3(total), block, 0, s, a);
+    else hipLaunchKernelGGL((k_sample_chunks<float, false>), dim3(total), block, 0, s, a);
+  }
   if (between != nullptr) {
     const hipError_t e = hipEventRecord(between, s);
     if (e != hipSuccess) return e;
   }
+  auto final_ = f64 ? (vec ? k_sample_final<double, true> : k_sample_final<double, false>)
+                    : (vec ? k_sample_final<float, true> : k_sample_final<float, false>);
   hipLaunchKernelGGL(final_, gf, block, 0, s, a);
   return hipGetLastError();
 }
