@@ -1,6 +1,5 @@
-// Building blocks of the fast path: a table-driven float64 exp, value-range
-// histograms with a descending bin walk for selection, and a bitonic sort
-// of LDS lists (used when many candidates share a value).
+// Building blocks of the fast path: a table-driven float64 exp and
+// value-range histograms with a descending bin walk for selection.
 #pragma once
 
 #include <limits.h>
@@ -19,12 +18,8 @@ namespace plh {
 constexpr double kLn2Hi = 6.93147180369123816490e-01;
 constexpr double kLn2Lo = 1.90821492927058770002e-10;
 
-__device__ __forceinline__ void init_exp_table(double* tab) {
-  if (threadIdx.x < 64) tab[threadIdx.x] = exp2((double)threadIdx.x / 64.0);
-}
-
-// The calling wave's own copy (needs no workgroup barrier before use: a
-// wave's LDS accesses complete in order).
+// The calling wave's own copy of the table (it needs no workgroup barrier
+// before use: a wave's LDS accesses complete in order).
 __device__ __forceinline__ void init_exp_table_wave(double* tab) {
   tab[lane()] = exp2((double)lane() / 64.0);
 }
@@ -66,46 +61,6 @@ __device__ __forceinline__ Affine make_affine(double lo, double hi, int nb) {
   a.scale = (hi > lo && hi - lo < INFINITY) ? (double)(nb - 1) / (hi - lo) : 0.0;
   if (!(a.scale < INFINITY)) a.scale = 0.0;
   return a;
-}
-
-// ------------------------------------------------------------ LDS sort
-// Bitonic sort of n <= N_max entries (key, idx, w) in LDS, into the order
-// where `before(ka, ia, kb, ib)` holds for earlier entries.  Entries past n
-// are padded with (pad_key, INT_MAX) which must sort last.
-template <class Before>
-__device__ __forceinline__ void lds_bitonic(uint64_t* key, int* idx, uint64_t* w, int n, uint64_t pad_key,
-                                            const Before& before) {
-  int N = 2;
-  while (N < n) N <<= 1;
-  for (int i = threadIdx.x; i < N; i += kThreads)
-    if (i >= n) {
-      key[i] = pad_key;
-      idx[i] = INT_MAX;
-      w[i] = 0ull;
-    }
-  wg_barrier();
-  for (int k = 2; k <= N; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < N; i += kThreads) {
-        const int ixj = i ^ j;
-        if (ixj > i) {
-          const uint64_t ka = key[i], kb = key[ixj];
-          const int ia = idx[i], ib = idx[ixj];
-          const bool sw = ((i & k) == 0) ? before(kb, ib, ka, ia) : before(ka, ia, kb, ib);
-          if (sw) {
-            key[i] = kb;
-            key[ixj] = ka;
-            idx[i] = ib;
-            idx[ixj] = ia;
-            const uint64_t t = w[i];
-            w[i] = w[ixj];
-            w[ixj] = t;
-          }
-        }
-      }
-      wg_barrier();
-    }
-  }
 }
 
 // Descending walk over nb histogram bins (counts and/or masses in LDS):

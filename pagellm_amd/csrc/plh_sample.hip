@@ -38,10 +38,14 @@ namespace plh {
 
 constexpr int kU = 8;             // 16-byte loads per thread per chunk
 constexpr int kHB = 1024;         // histogram bins
-constexpr int kSortMax = 2048;    // LDS sort list
-constexpr int kCandCap = 8192;    // candidates one row gathers in LDS
+constexpr int kCandCap = 8192;    // candidates one row gathers
 constexpr int kCapChunk = 1024;   // candidate slots per chunk, at most
-constexpr int kSelLevels = 4;
+constexpr int kMaxChunks = 64;    // chunks per row, at most (V <= 262144)
+constexpr int kMaxLevels = 12;    // histogram levels of one selection
+constexpr int kHBuf = 3;          // rotating histogram buffers of the merge
+constexpr int kDrawSpanMax = 256; // tokens per draw bin, at most (V <= 262144)
+constexpr int kSegPerLane = 8;    // segments per lane of one wave (V <= 262144)
+constexpr int kHistBatch = 8;     // history ids a thread loads at once
 
 // Chunk geometry per input type: a wave-wide 16-byte load covers kSpan
 // consecutive tokens, a wave owns one contiguous segment of kSeg tokens and
@@ -56,28 +60,28 @@ struct Geo {
 };
 constexpr int kSegMax = Geo<float>::kSeg;
 
-struct SortList {
-  uint64_t key[kSortMax];
-  uint64_t w[kSortMax];
-  int idx[kSortMax];
+struct Hist {
+  uint32_t cnt[kHB];
+  uint64_t mass[kHB];
+};
+
+// Candidates of a selection's last level, ranked by every wave.
+struct RankList {
+  uint64_t key[kWave];
+  uint64_t w[kWave];
+  int idx[kWave];
+  int n;
 };
 
 // LDS of k_sample_final (the candidates themselves stay in registers).
 struct FastSmem {
-  double redd[kWaves];
-  double redm[2 * kWaves];
-  uint64_t redu[kWaves];
-  int redi[kWaves];
-  int ctl[8];
-  uint64_t ctlu[4];
-  double exp_tab[64];
-  int cnt_c[64];
-  uint32_t hcnt[kHB];
-  uint64_t hmass[kHB];
-  union {
-    uint32_t segbits[kSegMax / 32];  // penalty bits of the rescanned segment
-    SortList sl;                     // selection and draw
-  } u;
+  uint64_t xw[4][3][kWaves];          // cross-wave combines
+  double exp_tab[kWaves][64];         // one exp table per wave
+  int wcnt[kWaves][kMaxChunks];       // per wave: candidate count of each chunk
+  Hist h[kHBuf];
+  uint64_t dspan[kDrawSpanMax];       // the draw's crossing bin, by token offset
+  RankList rl[2];                     // top-k, top-p
+  uint32_t segbits[kSegMax / 32];     // penalty bits of a rescanned segment
 };
 
 union SmemAll {
@@ -85,8 +89,6 @@ union SmemAll {
   Smem g;
 };
 
-// Workgroup barrier ordering LDS only (wg_barrier).
-__device__ __forceinline__ void lds_barrier() { wg_barrier(); }
 
 __device__ __forceinline__ RowParams load_row_params(const SampleArgs& a, int row) {
   RowParams rp;
@@ -125,10 +127,11 @@ __global__ __launch_bounds__(kThreads) void k_sample_rows(SampleArgs a) {
   if (threadIdx.x == 0) a.out_ids[row] = id;
 }
 
-// y = z / T as the segment partials compute it (multiplication by 1/T).
+// y = z / T as the segment partials compute it: multiplication by 1/T
+// (exact for T = 1).
 struct YScale {
   double T, invT;
-  __device__ __forceinline__ double operator()(double z) const { return T == 1.0 ? z : z * invT; }
+  __device__ __forceinline__ double operator()(double z) const { return z * invT; }
 };
 
 // ================================================================ chunks
@@ -201,12 +204,22 @@ __device__ __forceinline__ uint32_t chunk_pbits(const SampleArgs& a, const RowPa
   using G = Geo<TIn>;
   constexpr int kWords = G::kChunk / 32;
   for (int w = threadIdx.x; w < kWords; w += kThreads) cm.bitmap[w] = 0u;
-  lds_barrier();
-  for (int64_t h = rp.h0 + threadIdx.x; h < rp.h1; h += kThreads) {
-    const int off = a.hist_ids[h] - c0;
-    if ((unsigned)off < (unsigned)G::kChunk) lds_or(&cm.bitmap[off >> 5], 1u << (off & 31));
+  wg_barrier();
+  // kHistBatch ids per thread per round, all loaded before any is used
+  for (int64_t h0 = rp.h0; h0 < rp.h1; h0 += kHistBatch * kThreads) {
+    int id[kHistBatch];
+#pragma unroll
+    for (int j = 0; j < kHistBatch; ++j) {
+      const int64_t h = h0 + j * kThreads + threadIdx.x;
+      id[j] = h < rp.h1 ? a.hist_ids[h] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kHistBatch; ++j) {
+      const int off = id[j] - c0;
+      if ((unsigned)off < (unsigned)G::kChunk) lds_or(&cm.bitmap[off >> 5], 1u << (off & 31));
+    }
   }
-  lds_barrier();
+  wg_barrier();
   uint32_t pb = 0;
   const int q0 = wave() * G::kSeg + lane() * G::kVW;
 #pragma unroll
@@ -245,7 +258,8 @@ struct ChunkToks {
   using G = Geo<TIn>;
   typename VecOf<TIn>::T v[kU];
   int po = 0, np = 0;
-  __device__ __forceinline__ double raw(int e) const { return (double)v[e / G::kVW][e % G::kVW]; }
+  __device__ __forceinline__ TIn rv(int e) const { return v[e / G::kVW][e % G::kVW]; }
+  __device__ __forceinline__ double raw(int e) const { return (double)rv(e); }
   // Called at the start of each pass: the compiler must then widen the
   // registers again instead of keeping a float64 copy of the chunk alive
   // across passes (64 more VGPRs, which would cost occupancy).
@@ -286,6 +300,46 @@ __device__ __forceinline__ bool set_aside_penalised(ChunkToks<TIn>& tk, uint32_t
   return false;
 }
 
+// Histogram bins of the register tokens in their input precision: the
+// bounds of a float64 Affine rounded to float (lo rounded down) for float
+// inputs.  Rounding in the float arithmetic moves a bin edge by at most
+// 2^-23 * 1024 bins, well inside the 0.01-bin margin of the threshold.
+template <typename TIn>
+struct InAffine {
+  Affine af;
+  __device__ __forceinline__ explicit InAffine(const Affine& a) : af(a) {}
+  __device__ __forceinline__ int bin(TIn x) const { return af.bin(x); }
+  __device__ __forceinline__ double lo() const { return af.lo; }
+  __device__ __forceinline__ double scale() const { return af.scale; }
+};
+template <>
+struct InAffine<float> {
+  float lo_f, scale_f;
+  int nb;
+  __device__ __forceinline__ explicit InAffine(const Affine& a) : nb(a.nb) {
+    lo_f = __double2float_rd(a.lo);
+    scale_f = (float)a.scale;
+    if (!(scale_f < INFINITY)) scale_f = 0.0f;
+  }
+  __device__ __forceinline__ int bin(float x) const {
+    if (!(x > lo_f)) return 0;
+    const float t = (x - lo_f) * scale_f;
+    if (t >= (float)(nb - 1)) return nb - 1;
+    return t > 0.0f ? (int)t : 0;
+  }
+  __device__ __forceinline__ double lo() const { return (double)lo_f; }
+  __device__ __forceinline__ double scale() const { return (double)scale_f; }
+};
+
+// The smallest input-precision value >= theta (every finite value when theta
+// is -inf): x >= in_threshold(theta) holds exactly when x is finite and
+// (double)x >= theta.
+template <typename TIn>
+__device__ __forceinline__ TIn in_threshold(double theta) {
+  if constexpr (sizeof(TIn) == 4) return fmaxf(__double2float_ru(theta), -3.402823466e38f);
+  else return fmax(theta, -1.7976931348623157e308);
+}
+
 // Candidates of one chunk: every finite z >= theta, with theta below the
 // chunk's target-th largest token (all finite tokens when there are fewer).
 //   top-k, k <= 512: the k-th largest of the workgroup's 512 per-thread
@@ -293,10 +347,12 @@ __device__ __forceinline__ bool set_aside_penalised(ChunkToks<TIn>& tk, uint32_t
 //     bounds the k-th largest token from below;
 //   otherwise: a value histogram of all the chunk's tokens.
 // theta is the lower edge of the histogram bin holding the target-th
-// largest (cm.hcnt is zeroed at kernel start).  Each wave writes its
-// candidates to a range of the chunk's slots and its part: the chunk's
-// largest z, the largest finite z of its segment not written, the end of
-// its slots.  lmax is the calling thread's largest z.
+// largest (cm.hcnt is zeroed at kernel start).  The passes over the
+// register tokens compare in the input precision (exact: a float converts
+// to float64 exactly).  Each wave writes its candidates to a range of the
+// chunk's slots and its part: the chunk's largest z, the largest finite z
+// of its segment not written, the end of its slots.  lmax is the calling
+// thread's largest z.
 template <typename TIn>
 __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax, const SampleArgs& a,
                                                  const RowParams& rp, int g, int c0, int flags, WavePart* wp,
@@ -312,12 +368,14 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
   if (by_max) {
     if (lmax > -INFINITY) lo = lmax;
   } else {
+    TIn m = (TIn)INFINITY;
     tk.new_pass();
 #pragma unroll
     for (int e = 0; e < kEpt; ++e) {
-      const double z = tk.raw(e);
-      if (z > -INFINITY) lo = fmin(lo, z);
+      const TIn x = tk.rv(e);
+      m = fmin(m, x > (TIn)(-INFINITY) ? x : (TIn)INFINITY);
     }
+    lo = (double)m;
     for (int i = 0; i < tk.np; ++i) {
       const double z = tk.pen_z(cm, i);
       if (z > -INFINITY) lo = fmin(lo, z);
@@ -329,37 +387,44 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
   double theta = -INFINITY;
   if (hi > -INFINITY) {
     const Affine af = make_affine(lo, hi, kHB);
+    const InAffine<TIn> rf(af);
+    double tlo = af.lo, tscale = af.scale;
     if (by_max) {
       if (lmax > -INFINITY) lds_add(&cm.hcnt[af.bin(lmax)], 1u);
     } else {
+      tlo = rf.lo();
+      tscale = rf.scale();
+      const Affine pf{tlo, tscale, kHB};  // the same bins in float64, for the penalised tokens
       tk.new_pass();
 #pragma unroll
       for (int e = 0; e < kEpt; ++e) {
-        const double z = tk.raw(e);
-        if (z > -INFINITY) lds_add(&cm.hcnt[af.bin(z)], 1u);
+        const TIn x = tk.rv(e);
+        if (x > (TIn)(-INFINITY)) lds_add(&cm.hcnt[rf.bin(x)], 1u);
       }
       for (int i = 0; i < tk.np; ++i) {
         const double z = tk.pen_z(cm, i);
-        if (z > -INFINITY) lds_add(&cm.hcnt[af.bin(z)], 1u);
+        if (z > -INFINITY) lds_add(&cm.hcnt[pf.bin(z)], 1u);
       }
     }
-    lds_barrier();
+    wg_barrier();
     const Pick pk = pick_desc<false>(cm.hcnt, nullptr, kHB, 0, target, cm.redu, cm.ctl, cm.ctlu);
     // every z with bin(z) >= d is >= lo + (d - 0.01) / scale (bin(z) is
-    // floor((z - lo) * scale) up to a few ulps); bin 0 starts at lo
-    if (pk.found) theta = pk.d > 0 ? af.lo + ((double)uniform(pk.d) - 0.01) / af.scale : lo;
+    // floor((z - lo) * scale) up to rounding); bin 0 starts at lo
+    if (pk.found) theta = pk.d > 0 ? tlo + ((double)uniform(pk.d) - 0.01) / tscale : lo;
   }
   theta = uniform(theta);
+  const TIn tin = in_threshold<TIn>(theta);
   uint32_t pm = 0;
-  double um = -INFINITY;
+  TIn umt = (TIn)(-INFINITY);
   tk.new_pass();
 #pragma unroll
   for (int e = 0; e < kEpt; ++e) {
-    const double z = tk.raw(e);
-    const bool fin = z > -INFINITY;
-    if (fin && z >= theta) pm |= 1u << e;
-    else if (fin) um = fmax(um, z);
+    const TIn x = tk.rv(e);
+    const bool kp = x >= tin;
+    pm |= kp ? 1u << e : 0u;
+    umt = fmax(umt, kp ? (TIn)(-INFINITY) : x);
   }
+  double um = (double)umt;
   uint32_t qm = 0;  // penalised tokens kept
   for (int i = 0; i < tk.np; ++i) {
     const double z = tk.pen_z(cm, i);
@@ -428,8 +493,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
   ChunkToks<TIn> tk;
   load_chunk<TIn, VEC>(x, a.V, c0, tk.v);
-  const double* tab = cm.exp_tab[wave()];
-  init_exp_table_wave(cm.exp_tab[wave()]);
   const bool cands = rp.topk || rp.topp;
   if (cands) {  // ordered before use by the first barrier of chunk_candidates
     for (int b = threadIdx.x; b < kHB; b += kThreads) cm.hcnt[b] = 0u;
@@ -442,10 +505,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   }
   WavePart* wp = a.ws.part + (size_t)g * kWaves + wave();
   if (rp.greedy) {
-    ArgMax best{-INFINITY, INT_MAX};
-    tk.new_pass();
+    // the register tokens compare exactly in the input precision: their
+    // max, then the lowest slot holding it
+    TIn m = (TIn)(-INFINITY);
 #pragma unroll
-    for (int e = 0; e < G::kEpt; ++e) best = argmax_merge(best, ArgMax{tk.raw(e), c0 + slot_q<TIn>(e)});
+    for (int e = 0; e < G::kEpt; ++e) m = fmax(m, tk.v[e / G::kVW][e % G::kVW]);
+    uint32_t eq = 0u;
+#pragma unroll
+    for (int e = 0; e < G::kEpt; ++e) eq |= tk.v[e / G::kVW][e % G::kVW] == m ? 1u << e : 0u;
+    ArgMax best{-INFINITY, INT_MAX};
+    if (eq != 0u) best = ArgMax{(double)m, c0 + slot_q<TIn>(__builtin_ctz(eq))};
     for (int i = 0; i < tk.np; ++i) best = argmax_merge(best, ArgMax{tk.pen_z(cm, i), tk.pen_tok(cm, i)});
     best = wave_argmax(best);
     if (lane() == 0) {
@@ -455,10 +524,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     }
     return;
   }
-  double lmax = -INFINITY;
+  const double* tab = cm.exp_tab[wave()];
+  init_exp_table_wave(cm.exp_tab[wave()]);
+  TIn lm = (TIn)(-INFINITY);
   tk.new_pass();
 #pragma unroll
-  for (int e = 0; e < G::kEpt; ++e) lmax = fmax(lmax, tk.raw(e));
+  for (int e = 0; e < G::kEpt; ++e) lm = fmax(lm, tk.rv(e));
+  double lmax = (double)lm;
   for (int i = 0; i < tk.np; ++i) lmax = fmax(lmax, tk.pen_z(cm, i));
   if (cands) chunk_candidates<TIn>(tk, lmax, a, rp, g, c0, flags, wp, cm);
   else if (lane() == 0) wp->flags = flags;
@@ -483,45 +555,166 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 
 // ================================================================ finish
 
-// Inclusive and exclusive scan of one double per thread, thread order,
-// fixed association.
-__device__ __forceinline__ double block_scan_d(double v, double* red, double* excl, double* total) {
+// ================================================================ finalize
+// k_sample_final runs one workgroup per row.  Facts every wave needs (the
+// chunk partials, the normaliser, the crossing bin of a histogram, the
+// winner of a rank list) are computed by each wave on its own from the same
+// data in the same order, so the waves agree without a barrier.  Barriers
+// remain only where the waves' candidates meet in one LDS structure: a
+// cross-wave combine, a histogram level, a rank list, the draw's bins.
+
+// Cross-wave combine with rotating LDS slots: combine i posts one word per
+// wave and value to slot i % 4 and reads the table after one barrier.
+// Combine i + 4 writes that slot again only after the barriers of combines
+// i+1 .. i+3, which no wave passes before finishing its reads of combine i.
+struct XWave {
+  uint64_t (*slot)[3][kWaves];
+  int n;
+  __device__ __forceinline__ const uint64_t (*post(uint64_t x, uint64_t y, uint64_t z))[kWaves] {
+    uint64_t (*s)[kWaves] = slot[n & 3];
+    ++n;
+    if (lane() == 0) {
+      s[0][wave()] = x;
+      s[1][wave()] = y;
+      s[2][wave()] = z;
+    }
+    wg_barrier();
+    return s;
+  }
+};
+
+__device__ __forceinline__ uint64_t bits_of(double d) { return __builtin_bit_cast(uint64_t, d); }
+__device__ __forceinline__ double dbl_of(uint64_t u) { return __builtin_bit_cast(double, u); }
+
+// Workgroup sum of doubles (waves left to right).
+__device__ __forceinline__ double xw_sum(XWave& xw, double v) {
+  const auto s = xw.post(bits_of(wave_sum(v)), 0, 0);
+  double r = 0.0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) r += dbl_of(s[0][w]);
+  return r;
+}
+
+// Workgroup inclusive scan of one double per thread in thread order; *excl
+// and *total receive the exclusive value and the total.
+__device__ __forceinline__ double xw_scan(XWave& xw, double v, double* excl, double* total) {
   const double x = wave_scan_incl(v, 0.0, OpAdd{});
   const double xe = wave_shift_up1(x, 0.0);
-  if (lane() == kWave - 1) red[wave()] = x;
-  wg_barrier();
+  const auto s = xw.post(bits_of(lane_value(x, kWave - 1)), 0, 0);
   double pre = 0.0, tot = 0.0;
+#pragma unroll
   for (int w = 0; w < kWaves; ++w) {
-    if (w < wave()) pre += red[w];
-    tot += red[w];
+    const double t = dbl_of(s[0][w]);
+    if (w < wave()) pre += t;
+    tot += t;
   }
-  wg_barrier();
   *excl = pre + xe;
   *total = tot;
   return pre + x;
 }
 
+__device__ __forceinline__ int xw_min(XWave& xw, int v) {
+  const auto s = xw.post((uint64_t)(uint32_t)wave_min(v), 0, 0);
+  int r = INT_MAX;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) r = min(r, (int)(uint32_t)s[0][w]);
+  return r;
+}
+
+__device__ __forceinline__ int xw_max(XWave& xw, int v) {
+  const auto s = xw.post((uint64_t)(uint32_t)wave_max(v), 0, 0);
+  int r = INT_MIN;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) r = max(r, (int)(uint32_t)s[0][w]);
+  return r;
+}
+
 // Candidates of one row, held in registers: thread t owns slots
 // q * kThreads + t (q < kPerT) of the row's gathered list; bit q of `valid`
-// marks a real candidate.  v[q] holds the penalised logit, later its exp.
+// marks a real candidate.  v[q] holds the penalised logit, then its
+// probability; w[q] its fixed-point weight.
 constexpr int kPerT = kCandCap / kThreads;
 struct RegCands {
   double v[kPerT];
+  uint64_t w[kPerT];
   int idx[kPerT];
   uint32_t valid;
 };
 
-// Value-range selection over the register-resident candidates: slot q of
-// each thread takes part when it is valid and elig(q) holds; val(q) places
-// it in histogram bins (monotone in the order), key(q) orders exactly, token
-// index ascending on equal keys.
-//   MASS=false: the target-th largest key;
-//   MASS=true : in (key desc, index asc) order the first candidate whose
-//               inclusive weight wt(q) reaches target.
-// Histogram levels narrow the active set until at most 64 candidates are
-// left; one wave then ranks them (each lane counts the entries ahead of its
-// own).  giveup: more than kSortMax candidates share one value at the cut
-// (the caller falls back to the general pipeline).
+// The next histogram buffer of the row (zeroed), and zeroing of the one
+// after it: buffer g % 3 is last read right after the barrier of use g, and
+// zeroed during use g + 2, after the barrier of use g + 1.
+__device__ __forceinline__ Hist& next_hist(FastSmem& fs, int& g) {
+  Hist& h = fs.h[g % kHBuf];
+  Hist& z = fs.h[(g + 1) % kHBuf];
+  for (int b = threadIdx.x; b < kHB; b += kThreads) {
+    z.cnt[b] = 0u;
+    z.mass[b] = 0ull;
+  }
+  ++g;
+  return h;
+}
+
+// Shift that maps a key span onto at most kHB bins.
+__device__ __forceinline__ int span_shift(uint64_t span) {
+  return span < (uint64_t)kHB ? 0 : 64 - __clzll((long long)span) - 10;
+}
+
+struct WPick {
+  bool found;
+  int d;           // the crossing bin
+  uint64_t above;  // the running total above it
+};
+
+// Per wave: descending walk over the kHB bins of h: the bin where the
+// running total from `above` first reaches target.  The running total is
+// non-decreasing, so one bin takes it from below target to target or more.
+// Lane l sums bins [16(63-l), 16(63-l)+16), reading them in an order rotated
+// by l so that the lanes spread over the LDS banks; the lane whose range
+// crosses then walks its bins alone.
+template <bool MASS>
+__device__ __forceinline__ WPick wave_pick_desc(const Hist& h, uint64_t above, uint64_t target) {
+  constexpr int kPer = kHB / kWave;
+  const int dlo = kPer * (kWave - 1 - lane());
+  uint64_t s = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int d = dlo + ((j + lane()) & (kPer - 1));
+    s += MASS ? h.mass[d] : (uint64_t)h.cnt[d];
+  }
+  const uint64_t incl = wave_scan_incl(s, (uint64_t)0, OpAdd{});
+  const uint64_t ex = incl - s;
+  const uint64_t tot = lane_value(incl, kWave - 1);
+  if (above >= target || above + tot < target) return WPick{false, -1, above + tot};
+  const int L = __builtin_ctzll(__ballot(above + ex < target && above + incl >= target));
+  int d = 0;
+  uint64_t ab = 0;
+  if (lane() == L) {
+    uint64_t run = above + ex;
+#pragma unroll
+    for (int j = kPer - 1; j >= 0; --j) {
+      const uint64_t v = MASS ? h.mass[dlo + j] : (uint64_t)h.cnt[dlo + j];
+      if (run < target && run + v >= target) {
+        d = dlo + j;
+        ab = run;
+      }
+      run += v;
+    }
+  }
+  return WPick{true, lane_value(d, L), lane_value(ab, L)};
+}
+
+// Selection over the register candidates in (key desc, token index asc)
+// order, for the slots in act:
+//   MASS=false: the target-th entry (its key; the top-k threshold);
+//   MASS=true : the first entry whose inclusive weight reaches target (the
+//               top-p cut).
+// Levels of exact key bins (kHB bins of 2^sh consecutive keys) narrow the
+// active set to the crossing bin until at most one wave of candidates is
+// left; each wave then ranks them (every lane counts the entries ahead of
+// its own).  A run of equal keys is ordered by token index: the level keys
+// become V-1-index.  giveup: the levels did not converge (the caller falls
+// back to the general pipeline).
 struct SelOut {
   bool found;
   bool giveup;
@@ -529,345 +722,302 @@ struct SelOut {
   int idx;
 };
 
-// Workgroup (min, max, count) in one barrier round.
-__device__ __forceinline__ void block_range(double* lo, double* hi, uint32_t* cnt, FastSmem& fs) {
-  double a = wave_min(*lo), b = wave_max(*hi);
-  uint32_t n = wave_sum(*cnt);
-  if (lane() == 0) {
-    fs.redm[wave()] = a;
-    fs.redm[kWaves + wave()] = b;
-    reinterpret_cast<uint32_t*>(fs.redu)[wave()] = n;
-  }
-  wg_barrier();
-  a = fs.redm[0];
-  b = fs.redm[kWaves];
-  n = reinterpret_cast<uint32_t*>(fs.redu)[0];
+template <bool MASS, class Key>
+__device__ __forceinline__ SelOut select_desc(uint32_t act, const RegCands& rc, const Key& key, uint64_t target,
+                                              int V, RankList& rl, FastSmem& fs, XWave& xw, int& hgen) {
+  uint64_t lo = ~0ull, hi = 0ull;
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) {
-    a = fmin(a, fs.redm[w]);
-    b = fmax(b, fs.redm[kWaves + w]);
-    n += reinterpret_cast<uint32_t*>(fs.redu)[w];
-  }
-  wg_barrier();
-  *lo = a;
-  *hi = b;
-  *cnt = n;
-}
-
-__device__ __forceinline__ bool key_desc_idx_asc(uint64_t ka, int ia, uint64_t kb, int ib) {
-  return ka > kb || (ka == kb && ia < ib);
-}
-
-// Histogram levels chosen so far (at most kSelLevels = 4), held in named
-// fields so they stay in registers.
-struct Levels {
-  Affine a0, a1, a2, a3;
-  int d0 = 0, d1 = 0, d2 = 0, d3 = 0;
-  int n = 0;
-  __device__ __forceinline__ bool match(double v) const {
-    if (n > 0 && a0.bin(v) != d0) return false;
-    if (n > 1 && a1.bin(v) != d1) return false;
-    if (n > 2 && a2.bin(v) != d2) return false;
-    if (n > 3 && a3.bin(v) != d3) return false;
-    return true;
-  }
-  __device__ __forceinline__ void push(const Affine& a, int d) {
-    if (n == 0) {
-      a0 = a;
-      d0 = d;
-    } else if (n == 1) {
-      a1 = a;
-      d1 = d;
-    } else if (n == 2) {
-      a2 = a;
-      d2 = d;
-    } else {
-      a3 = a;
-      d3 = d;
+  for (int q = 0; q < kPerT; ++q)
+    if ((act >> q) & 1u) {
+      const uint64_t k = key(q);
+      lo = k < lo ? k : lo;
+      hi = k > hi ? k : hi;
     }
-    ++n;
-  }
-};
-static_assert(kSelLevels == 4, "Levels holds four histogram levels");
-
-template <bool MASS, class Elig, class Val, class Key, class W>
-__device__ __forceinline__ SelOut cand_select(const RegCands& rc, const Elig& elig, const Val& val, const Key& key,
-                                              const W& wt, uint64_t target, FastSmem& fs) {
-  Levels lv;
-  uint64_t above = 0;
-  SortList& sl = fs.u.sl;
-  for (;;) {
-    double lo = INFINITY, hi = -INFINITY;
-    uint32_t cnt = 0, act = 0;
+  {
+    const auto s = xw.post(wave_min(lo), wave_max(hi), (uint64_t)wave_sum((uint32_t)__popc(act)));
+    lo = s[0][0];
+    hi = s[1][0];
+    uint64_t n = s[2][0];
 #pragma unroll
-    for (int q = 0; q < kPerT; ++q) {
-      if (((rc.valid >> q) & 1u) && elig(q)) {
-        const double v = val(q);
-        if (lv.match(v)) {
-          lo = fmin(lo, v);
-          hi = fmax(hi, v);
-          ++cnt;
-          act |= 1u << q;
-        }
+    for (int w = 1; w < kWaves; ++w) {
+      lo = s[0][w] < lo ? s[0][w] : lo;
+      hi = s[1][w] > hi ? s[1][w] : hi;
+      n += s[2][w];
+    }
+    lo = uniform(lo);
+    hi = uniform(hi);
+    if (n == 0 || (!MASS && n < target)) return SelOut{false, false, 0, 0};
+    target = uniform(target);
+    uint32_t cnt = (uint32_t)uniform(n);
+    uint64_t above = 0;
+    bool by_idx = false;
+    auto lkey = [&](int q) -> uint64_t { return by_idx ? (uint64_t)(V - 1 - rc.idx[q]) : key(q); };
+    for (int lev = 0; cnt > (uint32_t)kWave; ++lev) {
+      if (lo == hi) {
+        if (!MASS) return SelOut{true, false, lo, 0};
+        if (by_idx) return SelOut{false, true, 0, 0};
+        by_idx = true;
+        lo = 0;
+        hi = (uint64_t)(V - 1);
       }
-    }
-    block_range(&lo, &hi, &cnt, fs);
-    if (cnt <= (uint32_t)kWave || !(hi > lo) || lv.n == kSelLevels) {
-      if (cnt > (uint32_t)kSortMax) return SelOut{false, true, 0, 0};
-      // list the active candidates: one LDS reservation per thread
-      if (threadIdx.x == 0) fs.ctl[2] = 0;
-      lds_barrier();
-      int slot = act ? lds_fetch_add(&fs.ctl[2], __popc(act)) : 0;
+      if (lev == kMaxLevels) return SelOut{false, true, 0, 0};
+      const int sh = span_shift(hi - lo);
+      Hist& h = next_hist(fs, hgen);
 #pragma unroll
       for (int q = 0; q < kPerT; ++q)
         if ((act >> q) & 1u) {
-          sl.key[slot] = key(q);
-          sl.idx[slot] = rc.idx[q];
-          sl.w[slot] = MASS ? wt(q) : 0ull;
-          ++slot;
+          const int b = (int)((lkey(q) - lo) >> sh);
+          lds_add(&h.cnt[b], 1u);
+          if (MASS) lds_add(&h.mass[b], rc.w[q]);
         }
-      lds_barrier();
-      const int m = (int)cnt;
-      if (m <= kWave) {
-        // one wave: each lane holds one entry and counts the entries ahead of
-        // it (rank) and their weight; the answer is the lane at rank pos, or
-        // the lane whose weight takes the running total across target
-        if (wave() == 0) {
-          const int ln = lane();
-          uint64_t k = 0ull, w = 0ull;
-          int ix = INT_MAX;
-          if (ln < m) {
-            k = sl.key[ln];
-            ix = sl.idx[ln];
-            w = sl.w[ln];
-          }
-          int rank = 0;
-          uint64_t ahead = 0;
-#pragma unroll 8
-          for (int j = 0; j < m; ++j) {
-            const bool bj = key_desc_idx_asc(sl.key[j], sl.idx[j], k, ix);
-            rank += bj ? 1 : 0;
-            if (MASS && bj) ahead += sl.w[j];
-          }
-          bool hit;
-          if (!MASS) hit = ln < m && (int64_t)rank == (int64_t)target - (int64_t)above - 1;
-          else hit = ln < m && above + ahead < target && above + ahead + w >= target;
-          const uint64_t b = __ballot(hit);
-          if (ln == 0) fs.ctl[3] = b != 0 ? 1 : 0;
-          if (hit) {
-            fs.ctlu[2] = k;
-            fs.ctl[4] = ix;
-          }
+      wg_barrier();
+      const WPick pk = wave_pick_desc<MASS>(h, above, target);
+      if (!pk.found) return SelOut{false, false, 0, 0};
+      above = uniform(pk.above);
+      const int d = uniform(pk.d);
+      cnt = (uint32_t)uniform((int)h.cnt[d]);
+      const uint64_t nlo = lo + ((uint64_t)d << sh);
+      const uint64_t wid = (1ull << sh) - 1;
+      const uint64_t nhi = hi - nlo < wid ? hi : nlo + wid;  // no wrap-around
+#pragma unroll
+      for (int q = 0; q < kPerT; ++q)
+        if ((act >> q) & 1u) {
+          const uint64_t k = lkey(q);
+          if (k < nlo || k > nhi) act &= ~(1u << q);
         }
-        lds_barrier();
-        const bool found = fs.ctl[3] != 0;
-        const SelOut r{found, !MASS && !found, found ? fs.ctlu[2] : 0ull, found ? fs.ctl[4] : 0};
-        lds_barrier();
-        return r;
-      }
-      lds_bitonic(sl.key, sl.idx, sl.w, m, 0ull, key_desc_idx_asc);
-      if (!MASS) {
-        const int pos = (int)(target - above - 1);
-        if (pos < 0 || pos >= m) return SelOut{false, true, 0, 0};
-        return SelOut{true, false, sl.key[pos], sl.idx[pos]};
-      }
-      // inclusive weight in sorted order, kSortMax / kThreads entries per thread
-      constexpr int kPer = kSortMax / kThreads;
-      const int i0 = kPer * (int)threadIdx.x;
-      uint64_t wl[kPer], s = 0;
-#pragma unroll
-      for (int q = 0; q < kPer; ++q) {
-        wl[q] = i0 + q < m ? sl.w[i0 + q] : 0ull;
-        s += wl[q];
-      }
-      uint64_t tot;
-      uint64_t run = above + block_excl_scan<uint64_t>(s, fs.redu, &tot);
-      int hit = INT_MAX;
-#pragma unroll
-      for (int q = 0; q < kPer; ++q) {
-        run += wl[q];
-        if (hit == INT_MAX && i0 + q < m && run >= target) hit = i0 + q;
-      }
-      hit = block_min<int>(hit, fs.redi);
-      if (hit == INT_MAX) return SelOut{false, false, 0, 0};
-      return SelOut{true, false, sl.key[hit], sl.idx[hit]};
+      lo = nlo;
+      hi = nhi;
     }
-    const Affine af = make_affine(lo, hi, kHB);
-    for (int b = threadIdx.x; b < kHB; b += kThreads) {
-      fs.hcnt[b] = 0u;
-      fs.hmass[b] = 0ull;
-    }
-    lds_barrier();
+    // rank list: one LDS reservation per wave
+    const int nq = __popc(act);
+    const int qi = wave_scan_incl(nq, 0, OpAdd{});
+    int rbase = 0;
+    if (lane() == kWave - 1 && qi > 0) rbase = lds_fetch_add(&rl.n, qi);
+    int slot = lane_value(rbase, kWave - 1) + qi - nq;
 #pragma unroll
     for (int q = 0; q < kPerT; ++q)
       if ((act >> q) & 1u) {
-        const int b = af.bin(val(q));
-        lds_add(&fs.hcnt[b], 1u);
-        if (MASS) lds_add(&fs.hmass[b], wt(q));
+        rl.key[slot] = key(q);
+        rl.idx[slot] = rc.idx[q];
+        rl.w[slot] = MASS ? rc.w[q] : 0ull;
+        ++slot;
       }
-    lds_barrier();
-    const Pick pk = pick_desc<MASS>(fs.hcnt, fs.hmass, kHB, above, target, fs.redu, fs.ctl, fs.ctlu);
-    if (!pk.found) return SelOut{false, false, 0, 0};
-    above = pk.above;
-    lv.push(af, pk.d);
+    wg_barrier();
+    const int m = uniform((int)cnt);
+    const int ln = lane();
+    uint64_t k = 0ull, w = 0ull;
+    int ix = INT_MAX;
+    if (ln < m) {
+      k = rl.key[ln];
+      ix = rl.idx[ln];
+      w = rl.w[ln];
+    }
+    int rank = 0;
+    uint64_t ahead = 0;
+#pragma unroll 8
+    for (int j = 0; j < m; ++j) {  // every lane reads entry j: LDS broadcast
+      const uint64_t kj = rl.key[j];
+      const int ij = rl.idx[j];
+      const bool bj = kj > k || (kj == k && ij < ix);
+      rank += bj ? 1 : 0;
+      if (MASS) ahead += bj ? rl.w[j] : 0ull;
+    }
+    bool hit;
+    if (!MASS) hit = ln < m && (uint64_t)rank == target - above - 1;
+    else hit = ln < m && above + ahead < target && above + ahead + w >= target;
+    const uint64_t hits = __ballot(hit);
+    if (hits == 0) return SelOut{false, !MASS, 0, 0};
+    const int L = __builtin_ctzll(hits);
+    return SelOut{true, false, lane_value(k, L), lane_value(ix, L)};
   }
 }
 
 // Inverse-CDF draw over the kept candidates in vocabulary order
-// (sampling.py:94-98): with w(q) the fixed-point probability of kept
-// candidates (0 otherwise), the first token whose running mass exceeds
-// floor(u * total); V-1 when none does.
-template <class W>
-__device__ __forceinline__ int draw_kept(const RegCands& rc, int V, double u, const W& wt, FastSmem& fs) {
-  auto wq = [&](int q) -> uint64_t { return ((rc.valid >> q) & 1u) ? wt(q) : 0ull; };
-  uint64_t tot = 0;
+// (sampling.py:94-98): with w[q] the fixed-point probability of kept slots
+// (0 otherwise), the first token whose running mass exceeds
+// floor(u * total); V-1 when none does.  Index bins of 2^sh consecutive
+// tokens locate the crossing bin; its tokens are then laid out by offset
+// and scanned.
+__device__ __forceinline__ int draw_kept(const RegCands& rc, int V, double u, FastSmem& fs, int& hgen) {
+  int sh = 0;
+  while (((V - 1) >> sh) >= kHB) ++sh;
+  Hist& h = next_hist(fs, hgen);
 #pragma unroll
-  for (int q = 0; q < kPerT; ++q) tot += wq(q);
-  tot = block_sum<uint64_t>(tot, fs.redu);
+  for (int q = 0; q < kPerT; ++q)
+    if (rc.w[q] != 0ull) lds_add(&h.mass[rc.idx[q] >> sh], rc.w[q]);
+  wg_barrier();
+  // lane l sums bins [16l, 16l+16) (rotated reads, as in wave_pick_desc)
+  constexpr int kPer = kHB / kWave;
+  const int b0 = kPer * lane();
+  uint64_t s = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) s += h.mass[b0 + ((j + lane()) & (kPer - 1))];
+  const uint64_t incl = wave_scan_incl(s, (uint64_t)0, OpAdd{});
+  const uint64_t tot = lane_value(incl, kWave - 1);
   if (tot == 0) return V - 1;
   const uint64_t t = (uint64_t)__double2ull_rd(u * (double)tot);
-  for (int b = threadIdx.x; b < kHB; b += kThreads) fs.hmass[b] = 0ull;
-  lds_barrier();
-  auto ibin = [&](int idx) -> int { return (int)(((int64_t)idx * kHB) / V); };
+  const uint64_t ex = incl - s;
+  const uint64_t hits = __ballot(ex <= t && t < incl);
+  if (hits == 0) return V - 1;
+  const int L = __builtin_ctzll(hits);
+  uint64_t bf = 0;
+  int bl = 0;
+  if (lane() == L) {
+    uint64_t run = ex;
 #pragma unroll
-  for (int q = 0; q < kPerT; ++q) {
-    const uint64_t w = wq(q);
-    if (w) lds_add(&fs.hmass[ibin(rc.idx[q])], w);
-  }
-  lds_barrier();
-  // first index bin whose running mass exceeds t (kHB / kThreads bins per thread)
-  constexpr int kPer = kHB / kThreads;
-  const int b0 = kPer * (int)threadIdx.x;
-  uint64_t hb[kPer], hs = 0;
-#pragma unroll
-  for (int q = 0; q < kPer; ++q) {
-    hb[q] = fs.hmass[b0 + q];
-    hs += hb[q];
-  }
-  uint64_t btot;
-  uint64_t brun = block_excl_scan<uint64_t>(hs, fs.redu, &btot);
-  // the running mass is non-decreasing: one bin takes it past t
-#pragma unroll
-  for (int q = 0; q < kPer; ++q) {
-    if (brun <= t && brun + hb[q] > t) {
-      fs.ctl[5] = b0 + q;
-      fs.ctlu[0] = brun;
-    }
-    brun += hb[q];
-  }
-  if (threadIdx.x == 0) fs.ctl[2] = 0;
-  wg_barrier();
-  if (btot <= t) return V - 1;
-  const int b = fs.ctl[5];
-  const uint64_t before = fs.ctlu[0];
-  SortList& sl = fs.u.sl;
-  uint32_t mine = 0;
-#pragma unroll
-  for (int q = 0; q < kPerT; ++q)
-    if (wq(q) && ibin(rc.idx[q]) == b) mine |= 1u << q;
-  int slot = mine ? lds_fetch_add(&fs.ctl[2], __popc(mine)) : 0;
-#pragma unroll
-  for (int q = 0; q < kPerT; ++q)
-    if ((mine >> q) & 1u) {
-      sl.key[slot] = (uint64_t)rc.idx[q];
-      sl.idx[slot] = rc.idx[q];
-      sl.w[slot] = wq(q);
-      ++slot;
-    }
-  lds_barrier();
-  const int m = fs.ctl[2];  // at most V / kHB + 1 <= kThreads tokens
-  if (m <= kWave) {
-    // one wave: each lane sums the weight of the entries with a smaller
-    // index; the hit is the lane whose weight takes the running mass past t
-    if (wave() == 0) {
-      const int ln = lane();
-      uint64_t w = 0ull;
-      int ix = INT_MAX;
-      if (ln < m) {
-        ix = sl.idx[ln];
-        w = sl.w[ln];
+    for (int j = 0; j < kPer; ++j) {
+      const uint64_t v = h.mass[b0 + j];
+      if (run <= t && t < run + v) {
+        bl = b0 + j;
+        bf = run;
       }
-      uint64_t ahead = 0;
-#pragma unroll 8
-      for (int j = 0; j < m; ++j)
-        if (sl.idx[j] < ix) ahead += sl.w[j];
-      const bool hit = ln < m && before + ahead <= t && before + ahead + w > t;
-      const uint64_t hbits = __ballot(hit);
-      if (ln == 0 && hbits == 0) fs.ctl[3] = INT_MAX;
-      if (hit) fs.ctl[3] = ix;
+      run += v;
     }
-    lds_barrier();
-    const int hit = fs.ctl[3];
-    return hit == INT_MAX ? V - 1 : hit;
   }
-  auto idx_asc = [](uint64_t ka, int, uint64_t kb, int) { return ka < kb; };
-  lds_bitonic(sl.key, sl.idx, sl.w, m, ~0ull, idx_asc);
-  const uint64_t w = (int)threadIdx.x < m ? sl.w[threadIdx.x] : 0ull;
-  uint64_t mt;
-  const uint64_t ex = block_excl_scan<uint64_t>(w, fs.redu, &mt);
-  const int hit = block_min<int>(((int)threadIdx.x < m && before + ex + w > t) ? sl.idx[threadIdx.x] : INT_MAX,
-                                 fs.redi);
-  return hit == INT_MAX ? V - 1 : hit;
+  const int b = uniform(lane_value(bl, L));
+  const uint64_t before = uniform(lane_value(bf, L));
+  // bin b's kept tokens by offset (fs.dspan is zero on entry)
+#pragma unroll
+  for (int q = 0; q < kPerT; ++q)
+    if (rc.w[q] != 0ull && (rc.idx[q] >> sh) == b) fs.dspan[rc.idx[q] - (b << sh)] = rc.w[q];
+  wg_barrier();
+  constexpr int kPs = kDrawSpanMax / kWave;
+  const int o0 = kPs * lane();
+  uint64_t ss = 0;
+#pragma unroll
+  for (int j = 0; j < kPs; ++j) ss += fs.dspan[o0 + ((j + (lane() >> 2)) & (kPs - 1))];
+  const uint64_t in2 = wave_scan_incl(ss, (uint64_t)0, OpAdd{});
+  const uint64_t e2 = before + in2 - ss;
+  const uint64_t h2 = __ballot(e2 <= t && t < before + in2);
+  if (h2 == 0) return V - 1;
+  const int L2 = __builtin_ctzll(h2);
+  int tok = 0;
+  if (lane() == L2) {
+    uint64_t r2 = e2;
+#pragma unroll
+    for (int j = 0; j < kPs; ++j) {
+      const uint64_t v = fs.dspan[o0 + j];
+      if (r2 <= t && t < r2 + v) tok = (b << sh) + o0 + j;
+      r2 += v;
+    }
+  }
+  return lane_value(tok, L2);
 }
 
-// Greedy rows: argmax over the segment argmaxes (lowest index on ties).
-__device__ __forceinline__ int finish_greedy(const SampleArgs& a, int row, FastSmem& fs) {
+// Per-wave summary of the row's wave partials (every wave reads them all).
+struct PartSum {
+  int flags;
+  double umax, zmax;
+  ArgMax best;
+};
+
+__device__ __forceinline__ PartSum scan_parts(const SampleArgs& a, int row, bool greedy, bool cands, FastSmem& fs) {
   const int P = a.ws.C * kWaves;
+  const WavePart* pp = a.ws.part + (size_t)row * P;
+  int* wc = fs.wcnt[wave()];
+  if (cands) wc[lane()] = 0;
+  int fl = 0;
+  double um = -INFINITY, zm = -INFINITY;
   ArgMax best{-INFINITY, INT_MAX};
-  for (int c = threadIdx.x; c < P; c += kThreads) {
-    const WavePart& p = a.ws.part[(size_t)row * P + c];
-    best = argmax_merge(best, ArgMax{p.best_z, p.best_idx});
+  for (int j = lane(); j < P; j += kWave) {
+    const WavePart& p = pp[j];
+    fl |= p.flags;
+    if (greedy) best = argmax_merge(best, ArgMax{p.best_z, p.best_idx});
+    if (cands) {
+      um = fmax(um, p.umax);
+      zm = fmax(zm, p.zmax);
+      lds_max(&wc[j / kWaves], p.end);  // a chunk's count: the largest end of its waves
+    }
   }
-  return block_argmax(best, fs.redd, fs.redi).i;
+  PartSum r;
+  r.flags = uniform(wave_max(fl));
+  r.umax = uniform(wave_max(um));
+  r.zmax = uniform(wave_max(zm));
+  r.best = greedy ? wave_argmax(best) : best;
+  return r;
 }
 
-// The full distribution's segment partials, one per thread (nseg <=
-// kThreads): *mk the segment max, *mass its sum rescaled to the largest
-// segment max, which goes to *ymax.
-__device__ __forceinline__ void segment_masses(const SampleArgs& a, int row, int nseg, FastSmem& fs, double* ymax,
-                                               double* mk, double* mass) {
-  const int k = threadIdx.x;
+// Full-distribution normaliser from the per-wave segment partials, by the
+// calling wave alone: lane l holds segments 8l .. 8l+7 (loaded by
+// load_segs), their masses rescaled to the largest segment max go to ms[],
+// and their exclusive prefix (segment order) to *lex.
+struct SegNorm {
+  double ymax, S;
+};
+
+struct SegLoad {
+  double mk[kSegPerLane], sk[kSegPerLane];
+};
+
+__device__ __forceinline__ void load_segs(const SampleArgs& a, int row, int nseg, SegLoad& sl) {
   const size_t b = (size_t)row * a.ws.C * kWaves;
-  *mk = k < nseg ? a.ws.seg_m[b + k] : -INFINITY;
-  const double sk = k < nseg ? a.ws.seg_s[b + k] : 0.0;
-  *ymax = block_max(*mk, fs.redd);
-  *mass = (k < nseg && *mk > -INFINITY) ? sk * fast_exp_neg(*mk - *ymax, fs.exp_tab) : 0.0;
+#pragma unroll
+  for (int j = 0; j < kSegPerLane; ++j) {
+    const int k = kSegPerLane * lane() + j;
+    sl.mk[j] = k < nseg ? a.ws.seg_m[b + k] : -INFINITY;
+    sl.sk[j] = k < nseg ? a.ws.seg_s[b + k] : 0.0;
+  }
+}
+
+__device__ __forceinline__ SegNorm seg_norm(const SegLoad& sl, const double* tab, double (&ms)[kSegPerLane],
+                                            double* lex) {
+  double ymax = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kSegPerLane; ++j) ymax = fmax(ymax, sl.mk[j]);
+  ymax = uniform(wave_max(ymax));
+  double ls = 0.0;
+#pragma unroll
+  for (int j = 0; j < kSegPerLane; ++j) {
+    ms[j] = sl.mk[j] > -INFINITY ? sl.sk[j] * fast_exp_neg(sl.mk[j] - ymax, tab) : 0.0;
+    ls += ms[j];
+  }
+  const double incl = wave_scan_incl(ls, 0.0, OpAdd{});
+  *lex = wave_shift_up1(incl, 0.0);
+  return SegNorm{ymax, uniform(lane_value(incl, kWave - 1))};
 }
 
 // Temperature only: full-vocabulary softmax and draw (sampling.py:75-81,
 // :94-98).  The segment holding the inverse-CDF point is rescanned from HBM
 // with the arithmetic of the partials.
 template <typename TIn>
-__device__ __forceinline__ int finish_temp(const SampleArgs& a, int row, const RowParams& rp, FastSmem& fs) {
+__device__ __forceinline__ int finish_temp(const SampleArgs& a, int row, const RowParams& rp, const SegLoad& sg,
+                                           FastSmem& fs, XWave& xw) {
   using G = Geo<TIn>;
   const int V = a.V;
-  const int nseg = (V + G::kSeg - 1) / G::kSeg;  // <= kThreads
   const YScale ys{rp.T, 1.0 / rp.T};
-  const int k = threadIdx.x;
-  double ymax, mk, mass;
-  segment_masses(a, row, nseg, fs, &ymax, &mk, &mass);
-  double ex, S;
-  block_scan_d(mass, fs.redd, &ex, &S);
-  const double t = rp.u * S;
-  const int kstar = block_min<int>((k < nseg && ex + mass > t) ? k : INT_MAX, fs.redi);
-  if (kstar == INT_MAX) return V - 1;
-  if (k == kstar) {
-    fs.ctlu[0] = (uint64_t)__double_as_longlong(ex);
-    fs.ctlu[1] = (uint64_t)__double_as_longlong(mk);
+  const double* tab = fs.exp_tab[wave()];
+  double ms[kSegPerLane], lex;
+  const SegNorm sn = seg_norm(sg, tab, ms, &lex);
+  const double t = rp.u * sn.S;
+  // the first segment whose running mass exceeds t
+  double run = lex, bl = 0.0, ml = 0.0;
+  int kl = INT_MAX;
+#pragma unroll
+  for (int j = 0; j < kSegPerLane; ++j) {
+    if (kl == INT_MAX && run + ms[j] > t) {
+      kl = kSegPerLane * lane() + j;
+      bl = run;
+      ml = sg.mk[j];
+    }
+    run += ms[j];
   }
+  const uint64_t hits = __ballot(kl != INT_MAX);
+  if (hits == 0) return V - 1;
+  const int L = __builtin_ctzll(hits);
+  const int kstar = uniform(lane_value(kl, L));
+  const double before = uniform(lane_value(bl, L));
+  const double mseg = uniform(lane_value(ml, L));
   const int s0 = kstar * G::kSeg;
   if (rp.pen_active) {
-    for (int w = threadIdx.x; w < G::kSeg / 32; w += kThreads) fs.u.segbits[w] = 0u;
+    for (int w = threadIdx.x; w < G::kSeg / 32; w += kThreads) fs.segbits[w] = 0u;
     wg_barrier();
     for (int64_t h = rp.h0 + threadIdx.x; h < rp.h1; h += kThreads) {
       const int off = a.hist_ids[h] - s0;
-      if ((unsigned)off < (unsigned)G::kSeg) lds_or(&fs.u.segbits[off >> 5], 1u << (off & 31));
+      if ((unsigned)off < (unsigned)G::kSeg) lds_or(&fs.segbits[off >> 5], 1u << (off & 31));
     }
+    wg_barrier();
   }
-  wg_barrier();
-  const double before = __longlong_as_double((long long)fs.ctlu[0]);
-  const double ms = __longlong_as_double((long long)fs.ctlu[1]);
-  const double sc = fast_exp_neg(ms - ymax, fs.exp_tab);
+  const double sc = fast_exp_neg(mseg - sn.ymax, tab);
   // thread t holds tokens s0 + kPer*t + q, in vocabulary order
   constexpr int kPer = G::kSeg / kThreads;
   const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
@@ -879,23 +1029,23 @@ __device__ __forceinline__ int finish_temp(const SampleArgs& a, int row, const R
     const int pos = s0 + q0 + q;
     if (pos < V) {
       double z = (double)x[pos];
-      if (rp.pen_active && ((fs.u.segbits[(q0 + q) >> 5] >> ((q0 + q) & 31)) & 1u)) z = penalize(z, rp.pen);
-      e[q] = fast_exp_neg(ys(z) - ms, fs.exp_tab);
+      if (rp.pen_active && ((fs.segbits[(q0 + q) >> 5] >> ((q0 + q) & 31)) & 1u)) z = penalize(z, rp.pen);
+      e[q] = fast_exp_neg(ys(z) - mseg, tab);
     }
     es += e[q];
   }
   double pex, ptot;
-  block_scan_d(es, fs.redd, &pex, &ptot);
-  double run = pex;
+  xw_scan(xw, es, &pex, &ptot);
+  double r = pex;
   int hit = INT_MAX, last = -1;
 #pragma unroll
   for (int q = 0; q < kPer; ++q) {
-    run += e[q];
+    r += e[q];
     if (e[q] > 0.0) last = s0 + q0 + q;
-    if (hit == INT_MAX && e[q] > 0.0 && before + run * sc > t) hit = s0 + q0 + q;
+    if (hit == INT_MAX && e[q] > 0.0 && before + r * sc > t) hit = s0 + q0 + q;
   }
-  hit = block_min<int>(hit, fs.redi);
-  if (hit == INT_MAX) hit = block_max<int>(last, fs.redi);  // rounding at the segment end
+  hit = xw_min(xw, hit);
+  if (hit == INT_MAX) hit = xw_max(xw, last);  // rounding at the segment end
   return hit < 0 ? V - 1 : hit;
 }
 
@@ -906,47 +1056,41 @@ struct FastOut {
 
 // Top-k and/or top-p rows (sampling.py:75-90, :94-98) from the gathered
 // chunk candidates.
-template <typename TIn, bool TOPK>
-__device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, int row, const RowParams& rp, FastSmem& fs) {
-  using G = Geo<TIn>;
-  const int V = a.V;
-  const int C = a.ws.C, capc = a.ws.capc;
-  // gather every slot of the row first (slot i = q * kThreads + t, chunk
-  // i / capc; consecutive lanes read consecutive addresses), then learn from
-  // the chunk partials which slots hold candidates
-  const int slots = C * capc;
+// Every candidate slot of the row into registers (slot i = q * kThreads + t;
+// consecutive lanes read consecutive addresses).
+__device__ __forceinline__ void gather_cands(const SampleArgs& a, int row, RegCands& rc) {
+  const int slots = a.ws.C * a.ws.capc;
   const size_t base = (size_t)row * slots;
-  RegCands rc;
-  rc.valid = 0;
 #pragma unroll
   for (int q = 0; q < kPerT; ++q) {
     const int i = q * kThreads + (int)threadIdx.x;
     rc.v[q] = 0.0;
     rc.idx[q] = 0;
+    rc.w[q] = 0ull;
     if (i < slots) {
       rc.v[q] = a.ws.cz[base + i];
       rc.idx[q] = a.ws.ci[base + i];
     }
   }
-  // a chunk's candidate count is the largest end over its waves
-  if ((int)threadIdx.x < C) fs.cnt_c[threadIdx.x] = 0;
-  wg_barrier();
-  double u_l = -INFINITY, zm_l = -INFINITY;
-  if ((int)threadIdx.x < C * kWaves) {
-    const WavePart p = a.ws.part[(size_t)row * C * kWaves + threadIdx.x];
-    lds_max(&fs.cnt_c[threadIdx.x / kWaves], p.end);
-    u_l = p.umax;
-    zm_l = p.zmax;
-  }
-  const double U = block_max(u_l, fs.redd);
-  const double zmax = block_max(zm_l, fs.redd);
+}
+
+template <typename TIn, bool TOPK>
+__device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, RegCands& rc, const SegLoad& sg,
+                                                const RowParams& rp, const PartSum& ps, FastSmem& fs, XWave& xw,
+                                                int& hgen) {
+  const int V = a.V;
+  const int capc = a.ws.capc;
+  const int csh = __ffs(capc) - 1;  // capc is a power of two
+  const int slots = a.ws.C * capc;
+  const double* tab = fs.exp_tab[wave()];
+  // slot i (chunk i / capc) holds a candidate when it lies below its
+  // chunk's count
+  const int* wc = fs.wcnt[wave()];
+  rc.valid = 0;
 #pragma unroll
   for (int q = 0; q < kPerT; ++q) {
     const int i = q * kThreads + (int)threadIdx.x;
-    if (i < slots) {
-      const int c = i / capc;
-      if (i - c * capc < fs.cnt_c[c]) rc.valid |= 1u << q;
-    }
+    if (i < slots && (i & (capc - 1)) < wc[i >> csh]) rc.valid |= 1u << q;
   }
   const double T = rp.T;
   auto yexact = [&](double z) -> double { return T == 1.0 ? z : z / T; };
@@ -954,9 +1098,8 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, int row, co
   // ---- top-k: k-th largest with multiplicity, keep y >= kth_y (:76-78)
   double z_lo = -INFINITY;
   if (TOPK) {
-    const SelOut r = cand_select<false>(rc, [](int) { return true; }, [&](int q) { return rc.v[q]; },
-                                        [&](int q) { return key_of(rc.v[q]); }, [](int) { return 0ull; },
-                                        (uint64_t)rp.top_k, fs);
+    const SelOut r = select_desc<false>(rc.valid, rc, [&](int q) { return key_of(rc.v[q]); }, (uint64_t)rp.top_k,
+                                        V, fs.rl[0], fs, xw, hgen);
     if (!r.found) return FastOut{V - 1, true};
     const double kth_z = val_of_key(r.key);
     const double kth_y = yexact(kth_z);
@@ -966,66 +1109,58 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, int row, co
       if (yexact(zp) >= kth_y) z_lo = zp;
       else break;
     }
-    if (!(U < z_lo)) return FastOut{V - 1, true};
+    if (!(ps.umax < z_lo)) return FastOut{V - 1, true};
   }
 
-  // ---- softmax (:79-81): each candidate's exp(y - ymax) once, in place of
-  // z (0 outside the top-k set); p = e / S
+  // ---- softmax (:79-81): p = exp(y - ymax) / S, once per candidate
   const YScale ys{T, 1.0 / T};
-  const double ymax = ys(zmax);
+  const double ymax = ys(ps.zmax);
   double s = 0.0;
 #pragma unroll
   for (int q = 0; q < kPerT; ++q) {
     const double z = rc.v[q];
-    const double e = (((rc.valid >> q) & 1u) && z >= z_lo) ? fast_exp_neg(ys(z) - ymax, fs.exp_tab) : 0.0;
+    const double e = (((rc.valid >> q) & 1u) && z >= z_lo) ? fast_exp_neg(ys(z) - ymax, tab) : 0.0;
     rc.v[q] = e;
     s += e;
   }
   double S;
   if (TOPK) {
-    S = block_sum(s, fs.redd);
+    S = xw_sum(xw, s);
   } else {
-    const int nseg = (V + G::kSeg - 1) / G::kSeg;
-    double ysmax, mk, mass;
-    segment_masses(a, row, nseg, fs, &ysmax, &mk, &mass);
-    S = block_sum(mass, fs.redd);
+    double ms[kSegPerLane], lex;
+    S = seg_norm(sg, tab, ms, &lex).S;
   }
   const double invS = 1.0 / S;
-  auto pq = [&](int q) -> double { return rc.v[q] * invS; };
+  uint32_t pos = 0;
+#pragma unroll
+  for (int q = 0; q < kPerT; ++q) {
+    rc.v[q] *= invS;
+    rc.w[q] = to_fx(rc.v[q]);
+    if (rc.v[q] > 0.0) pos |= 1u << q;
+  }
 
   // ---- top-p: first token (p desc, index asc) whose inclusive mass reaches
-  // top_p (:82-90); bins on the bit pattern of p (log-spaced)
-  bool have_cut = false;
-  uint64_t cut_key = 0;
-  int cut_idx = INT_MAX;
+  // top_p (:82-90)
   if (rp.topp) {
-    const SelOut r = cand_select<true>(rc, [&](int q) { return rc.v[q] > 0.0; },
-                                       [&](int q) { return (double)pkey_of(pq(q)); },
-                                       [&](int q) { return pkey_of(pq(q)); }, [&](int q) { return to_fx(pq(q)); },
-                                       topp_target(rp.top_p), fs);
+    const SelOut r = select_desc<true>(pos, rc, [&](int q) { return pkey_of(rc.v[q]); }, topp_target(rp.top_p), V,
+                                       fs.rl[1], fs, xw, hgen);
     if (r.giveup) return FastOut{V - 1, true};
     if (r.found) {
-      have_cut = true;
-      cut_key = r.key;
-      cut_idx = r.idx;
+#pragma unroll
+      for (int q = 0; q < kPerT; ++q) {
+        const uint64_t k = pkey_of(rc.v[q]);
+        if (!(k > r.key || (k == r.key && rc.idx[q] <= r.idx))) rc.w[q] = 0ull;
+      }
     }
-    if (!TOPK && U > -INFINITY) {
-      const double pU = fast_exp_neg(ys(U) - ymax, fs.exp_tab) * invS;
-      if (!(have_cut && cut_key > pkey_of(pU))) return FastOut{V - 1, true};
+    if (!TOPK && ps.umax > -INFINITY) {
+      // the largest token left out must fall outside the nucleus
+      const double pU = fast_exp_neg(ys(ps.umax) - ymax, tab) * invS;
+      if (!(r.found && r.key > pkey_of(pU))) return FastOut{V - 1, true};
     }
   }
 
   // ---- draw in vocabulary order (:94-98)
-  auto wt = [&](int q) -> uint64_t {
-    const double p = pq(q);
-    if (!(p > 0.0)) return 0ull;
-    if (have_cut) {
-      const uint64_t k = pkey_of(p);
-      if (!(k > cut_key || (k == cut_key && rc.idx[q] <= cut_idx))) return 0ull;
-    }
-    return to_fx(p);
-  };
-  return FastOut{draw_kept(rc, V, rp.u, wt, fs), false};
+  return FastOut{draw_kept(rc, V, rp.u, fs, hgen), false};
 }
 
 template <typename TIn, bool VEC>
@@ -1034,21 +1169,38 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   FastSmem& fs = sm.f;
   const int row = blockIdx.x;
   const RowParams rp = load_row_params(a, row);
-  init_exp_table(fs.exp_tab);
-  wg_barrier();
-  int id = 0;
+  init_exp_table_wave(fs.exp_tab[wave()]);
+  const bool cands = !rp.greedy && (rp.topk || rp.topp);
+  if (cands) {  // ordered before their first use by the first barrier
+    for (int b = threadIdx.x; b < kHB; b += kThreads) {
+      fs.h[0].cnt[b] = 0u;
+      fs.h[0].mass[b] = 0ull;
+    }
+    if (threadIdx.x < kDrawSpanMax) fs.dspan[threadIdx.x] = 0ull;
+    if (threadIdx.x < 2) fs.rl[threadIdx.x].n = 0;
+  }
+  XWave xw{fs.xw, 0};
+  int hgen = 0;
+  // global loads first: candidates, segment partials, then the wave parts
+  RegCands rc;
+  if (cands) gather_cands(a, row, rc);
+  SegLoad sg;
+  if (!rp.greedy && !rp.topk) {
+    load_segs(a, row, (a.V + Geo<TIn>::kSeg - 1) / Geo<TIn>::kSeg, sg);
+  }
+  const PartSum ps = scan_parts(a, row, rp.greedy, cands, fs);
   // a chunk that could not keep all its penalised tokens aside sends the
   // row to the general pipeline
-  int fl = 0;
-  for (int c = threadIdx.x; c < a.ws.C * kWaves; c += kThreads) fl |= a.ws.part[(size_t)row * a.ws.C * kWaves + c].flags;
-  bool general = block_max<int>(fl, fs.redi) != 0;
+  bool general = ps.flags != 0;
+  int id = 0;
   if (general) {
   } else if (rp.greedy) {
-    id = finish_greedy(a, row, fs);
-  } else if (!rp.topk && !rp.topp) {
-    id = finish_temp<TIn>(a, row, rp, fs);
+    id = ps.best.i;
+  } else if (!cands) {
+    id = finish_temp<TIn>(a, row, rp, sg, fs, xw);
   } else {
-    const FastOut o = rp.topk ? finish_cands<TIn, true>(a, row, rp, fs) : finish_cands<TIn, false>(a, row, rp, fs);
+    const FastOut o = rp.topk ? finish_cands<TIn, true>(a, rc, sg, rp, ps, fs, xw, hgen)
+                              : finish_cands<TIn, false>(a, rc, sg, rp, ps, fs, xw, hgen);
     id = o.id;
     general = o.general;
   }
