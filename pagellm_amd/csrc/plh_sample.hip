@@ -154,7 +154,7 @@ struct VecOf<double> {
 // pipeline).
 constexpr int kPenPerWave = 128;
 
-// LDS of k_sample_chunks: about 23 KB.
+// LDS of k_sample_chunks: about 35 KB.
 struct ChunkSmem {
   double redd[2 * kWaves];
   uint64_t redu[kWaves];
@@ -166,6 +166,8 @@ struct ChunkSmem {
   uint32_t bitmap[Geo<float>::kChunk / 32];
   double pz[kWaves][kPenPerWave];
   int pt[kWaves][kPenPerWave];
+  double sz[kCapChunk];  // candidates staged on their way to the workspace
+  int si[kCapChunk];
   int cand_n;
 };
 
@@ -290,13 +292,15 @@ __device__ __forceinline__ bool set_aside_penalised(ChunkToks<TIn>& tk, uint32_t
 #pragma unroll
     for (int e = 0; e < G::kEpt; ++e) {
       if ((pb >> e) & 1u) {
-        cm.pz[wave()][k] = penalize(tk.raw(e), pen);
+        cm.pz[wave()][k] = tk.raw(e);
         cm.pt[wave()][k] = c0 + slot_q<TIn>(e);
         ++k;
         tk.v[e / G::kVW][e % G::kVW] = (TIn)(-INFINITY);
       }
     }
   }
+  // penalised afterwards, a few entries per lane (a division each)
+  for (int i = 0; i < tk.np; ++i) cm.pz[wave()][tk.po + i] = penalize(cm.pz[wave()][tk.po + i], pen);
   return false;
 }
 
@@ -439,16 +443,16 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
   int base = 0;
   if (lane() == kWave - 1) base = lds_fetch_add(&cm.cand_n, incl);
   base = lane_value(base, kWave - 1);
+  // the wave's candidates go to its slots [base, base + wtot) in LDS first,
+  // then to the workspace with consecutive lanes on consecutive slots
   int slot = base + incl - cnt;
-  double* cz = a.ws.cz + (size_t)g * capc;
-  int32_t* ci = a.ws.ci + (size_t)g * capc;
   tk.new_pass();
 #pragma unroll
   for (int e = 0; e < kEpt; ++e) {
     if ((pm >> e) & 1u) {
       if (slot < capc) {
-        cz[slot] = tk.raw(e);
-        ci[slot] = c0 + slot_q<TIn>(e);
+        cm.sz[slot] = tk.raw(e);
+        cm.si[slot] = c0 + slot_q<TIn>(e);
       } else {
         um = fmax(um, tk.raw(e));
       }
@@ -458,19 +462,26 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
   for (int i = 0; i < tk.np; ++i) {
     if ((qm >> i) & 1u) {
       if (slot < capc) {
-        cz[slot] = tk.pen_z(cm, i);
-        ci[slot] = tk.pen_tok(cm, i);
+        cm.sz[slot] = tk.pen_z(cm, i);
+        cm.si[slot] = tk.pen_tok(cm, i);
       } else {
         um = fmax(um, tk.pen_z(cm, i));
       }
       ++slot;
     }
   }
+  const int wend = min(base + wtot, capc);
+  double* cz = a.ws.cz + (size_t)g * capc;
+  int32_t* ci = a.ws.ci + (size_t)g * capc;
+  for (int i = base + lane(); i < wend; i += kWave) {
+    cz[i] = cm.sz[i];
+    ci[i] = cm.si[i];
+  }
   um = wave_max(um);
   if (lane() == 0) {
     wp->zmax = hi;
     wp->umax = um;
-    wp->end = min(base + wtot, capc);
+    wp->end = wend;
     wp->flags = flags;
   }
 }
