@@ -11,7 +11,7 @@ namespace plh {
 // chunk) for k_sample_final.
 struct WavePart {
   double zmax;    // largest finite penalised logit of the segment (-inf if none)
-  double umax;    // largest finite one not kept as a candidate (-inf if none)
+  double umax;    // bound on the tokens not kept as candidates: all are below it
   double best_z;  // greedy rows: the segment's argmax value ...
   int best_idx;   // ... and its token id
   int end;        // candidate rows: end of the wave's slots in its chunk's list

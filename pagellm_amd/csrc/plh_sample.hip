@@ -70,6 +70,8 @@ struct RankList {
   uint64_t key[kWave];
   uint64_t w[kWave];
   int idx[kWave];
+  uint32_t rank[kWave];   // entries ahead of each entry ...
+  uint64_t ahead[kWave];  // ... and their weight (summed over the waves)
   int n;
 };
 
@@ -162,7 +164,7 @@ struct ChunkSmem {
   int ctl[8];
   uint64_t ctlu[4];
   double exp_tab[kWaves][64];  // one copy per wave
-  uint32_t hcnt[kHB];
+  uint32_t hcnt[kHB + 1];  // bin kHB: -inf tokens (never scanned)
   uint32_t bitmap[Geo<float>::kChunk / 32];
   double pz[kWaves][kPenPerWave];
   int pt[kWaves][kPenPerWave];
@@ -313,6 +315,8 @@ struct InAffine {
   Affine af;
   __device__ __forceinline__ explicit InAffine(const Affine& a) : af(a) {}
   __device__ __forceinline__ int bin(TIn x) const { return af.bin(x); }
+  // bin(x) for finite x, af.nb for -inf
+  __device__ __forceinline__ int bin_or_discard(TIn x) const { return x > -INFINITY ? af.bin(x) : af.nb; }
   __device__ __forceinline__ double lo() const { return af.lo; }
   __device__ __forceinline__ double scale() const { return af.scale; }
 };
@@ -325,11 +329,16 @@ struct InAffine<float> {
     scale_f = (float)a.scale;
     if (!(scale_f < INFINITY)) scale_f = 0.0f;
   }
+  // finite x >= lo_f: the scaled offset is >= 0 and the median clamps it
+  // to [0, nb - 1]
   __device__ __forceinline__ int bin(float x) const {
-    if (!(x > lo_f)) return 0;
-    const float t = (x - lo_f) * scale_f;
-    if (t >= (float)(nb - 1)) return nb - 1;
-    return t > 0.0f ? (int)t : 0;
+    return (int)__builtin_amdgcn_fmed3f((x - lo_f) * scale_f, 0.0f, (float)(nb - 1));
+  }
+  // bin(x) for finite x, nb for -inf, without a branch: x >= lo_f makes
+  // the scaled offset >= 0, and the median clamps it to [0, nb - 1]
+  __device__ __forceinline__ int bin_or_discard(float x) const {
+    const float t = __builtin_amdgcn_fmed3f((x - lo_f) * scale_f, 0.0f, (float)(nb - 1));
+    return x > -INFINITY ? (int)t : nb;
   }
   __device__ __forceinline__ double lo() const { return (double)lo_f; }
   __device__ __forceinline__ double scale() const { return (double)scale_f; }
@@ -349,14 +358,19 @@ __device__ __forceinline__ TIn in_threshold(double theta) {
 //   top-k, k <= 512: the k-th largest of the workgroup's 512 per-thread
 //     maxima is itself k tokens deep, so a histogram of those maxima alone
 //     bounds the k-th largest token from below;
-//   otherwise: a value histogram of all the chunk's tokens.
+//   otherwise: a value histogram of the chunk's tokens from L up, where L
+//     is the smallest per-thread second-largest register token: each of
+//     the n2 threads holding two finite ones has two tokens >= L, so when
+//     2 * n2 >= target the target-th largest is >= L and the tokens below
+//     L (typically three quarters) take no LDS atomic; else L is the
+//     smallest finite token.
 // theta is the lower edge of the histogram bin holding the target-th
-// largest (cm.hcnt is zeroed at kernel start).  The passes over the
-// register tokens compare in the input precision (exact: a float converts
-// to float64 exactly).  Each wave writes its candidates to a range of the
-// chunk's slots and its part: the chunk's largest z, the largest finite z
-// of its segment not written, the end of its slots.  lmax is the calling
-// thread's largest z.
+// largest (cm.hcnt is zeroed at kernel start), so every token left out is
+// below theta, which serves as the chunk's bound on them.  The passes over
+// the register tokens compare in the input precision (exact: a float
+// converts to float64 exactly).  Each wave writes its candidates to a range
+// of the chunk's slots and its part: the chunk's largest z, theta, the end
+// of its slots.  lmax is the calling thread's largest z.
 template <typename TIn>
 __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax, const SampleArgs& a,
                                                  const RowParams& rp, int g, int c0, int flags, WavePart* wp,
@@ -371,21 +385,57 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
   double lo = INFINITY, hi = lmax;
   if (by_max) {
     if (lmax > -INFINITY) lo = lmax;
+    block_minmax(&lo, &hi, cm.redd);
   } else {
-    TIn m = (TIn)INFINITY;
+    TIn m1 = (TIn)(-INFINITY), m2 = (TIn)(-INFINITY);
     tk.new_pass();
 #pragma unroll
     for (int e = 0; e < kEpt; ++e) {
       const TIn x = tk.rv(e);
-      m = fmin(m, x > (TIn)(-INFINITY) ? x : (TIn)INFINITY);
+      m2 = fmax(m2, fmin(m1, x));
+      m1 = fmax(m1, x);
     }
-    lo = (double)m;
-    for (int i = 0; i < tk.np; ++i) {
-      const double z = tk.pen_z(cm, i);
-      if (z > -INFINITY) lo = fmin(lo, z);
+    // one barrier round: min of the finite m2, their count, max of lmax
+    double l2 = m2 > (TIn)(-INFINITY) ? (double)m2 : INFINITY;
+    int n2 = m2 > (TIn)(-INFINITY) ? 1 : 0;
+    l2 = wave_min(l2);
+    hi = wave_max(hi);
+    n2 = wave_sum(n2);
+    if (lane() == 0) {
+      cm.redd[wave()] = l2;
+      cm.redd[kWaves + wave()] = hi;
+      cm.redi[wave()] = n2;
+    }
+    wg_barrier();
+    l2 = cm.redd[0];
+    hi = cm.redd[kWaves];
+    n2 = cm.redi[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+      l2 = fmin(l2, cm.redd[w]);
+      hi = fmax(hi, cm.redd[kWaves + w]);
+      n2 += cm.redi[w];
+    }
+    if (2 * (uint64_t)uniform(n2) >= target) {
+      lo = l2;
+    } else {  // few finite tokens: L is the smallest one
+      TIn m = (TIn)INFINITY;
+      tk.new_pass();
+#pragma unroll
+      for (int e = 0; e < kEpt; ++e) {
+        const TIn x = tk.rv(e);
+        m = fmin(m, x > (TIn)(-INFINITY) ? x : (TIn)INFINITY);
+      }
+      lo = (double)m;
+      for (int i = 0; i < tk.np; ++i) {
+        const double z = tk.pen_z(cm, i);
+        if (z > -INFINITY) lo = fmin(lo, z);
+      }
+      double h2 = hi;
+      wg_barrier();  // the reads of cm.redd above are done
+      block_minmax(&lo, &h2, cm.redd);
     }
   }
-  block_minmax(&lo, &hi, cm.redd);
   lo = uniform(lo);
   hi = uniform(hi);
   double theta = -INFINITY;
@@ -399,15 +449,16 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
       tlo = rf.lo();
       tscale = rf.scale();
       const Affine pf{tlo, tscale, kHB};  // the same bins in float64, for the penalised tokens
+      const TIn lin = in_threshold<TIn>(lo);
       tk.new_pass();
 #pragma unroll
       for (int e = 0; e < kEpt; ++e) {
         const TIn x = tk.rv(e);
-        if (x > (TIn)(-INFINITY)) lds_add(&cm.hcnt[rf.bin(x)], 1u);
+        if (x >= lin) lds_add(&cm.hcnt[rf.bin(x)], 1u);
       }
       for (int i = 0; i < tk.np; ++i) {
         const double z = tk.pen_z(cm, i);
-        if (z > -INFINITY) lds_add(&cm.hcnt[pf.bin(z)], 1u);
+        if (z > -INFINITY && z >= lo) lds_add(&cm.hcnt[pf.bin(z)], 1u);
       }
     }
     wg_barrier();
@@ -419,22 +470,13 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
   theta = uniform(theta);
   const TIn tin = in_threshold<TIn>(theta);
   uint32_t pm = 0;
-  TIn umt = (TIn)(-INFINITY);
   tk.new_pass();
 #pragma unroll
-  for (int e = 0; e < kEpt; ++e) {
-    const TIn x = tk.rv(e);
-    const bool kp = x >= tin;
-    pm |= kp ? 1u << e : 0u;
-    umt = fmax(umt, kp ? (TIn)(-INFINITY) : x);
-  }
-  double um = (double)umt;
+  for (int e = 0; e < kEpt; ++e) pm |= tk.rv(e) >= tin ? 1u << e : 0u;
   uint32_t qm = 0;  // penalised tokens kept
   for (int i = 0; i < tk.np; ++i) {
     const double z = tk.pen_z(cm, i);
-    const bool fin = z > -INFINITY;
-    if (fin && z >= theta) qm |= 1u << i;
-    else if (fin) um = fmax(um, z);
+    if (z > -INFINITY && z >= theta) qm |= 1u << i;
   }
   // one LDS reservation per wave (cm.cand_n was reset before the barriers above)
   const int cnt = __popc(pm) + __popc(qm);
@@ -444,43 +486,41 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
   if (lane() == kWave - 1) base = lds_fetch_add(&cm.cand_n, incl);
   base = lane_value(base, kWave - 1);
   // the wave's candidates go to its slots [base, base + wtot) in LDS first,
-  // then to the workspace with consecutive lanes on consecutive slots
-  int slot = base + incl - cnt;
-  tk.new_pass();
+  // then to the workspace with consecutive lanes on consecutive slots; a
+  // wave whose slots would run past capc makes the chunk incomplete
+  int wend = base + wtot;
+  if (wend > capc) {
+    flags |= kChunkIncomplete;
+    wend = base;
+  } else {
+    int slot = base + incl - cnt;
+    tk.new_pass();
 #pragma unroll
-  for (int e = 0; e < kEpt; ++e) {
-    if ((pm >> e) & 1u) {
-      if (slot < capc) {
+    for (int e = 0; e < kEpt; ++e) {
+      if ((pm >> e) & 1u) {
         cm.sz[slot] = tk.raw(e);
         cm.si[slot] = c0 + slot_q<TIn>(e);
-      } else {
-        um = fmax(um, tk.raw(e));
+        ++slot;
       }
-      ++slot;
     }
-  }
-  for (int i = 0; i < tk.np; ++i) {
-    if ((qm >> i) & 1u) {
-      if (slot < capc) {
+    for (int i = 0; i < tk.np; ++i) {
+      if ((qm >> i) & 1u) {
         cm.sz[slot] = tk.pen_z(cm, i);
         cm.si[slot] = tk.pen_tok(cm, i);
-      } else {
-        um = fmax(um, tk.pen_z(cm, i));
+        ++slot;
       }
-      ++slot;
+    }
+    double* cz = a.ws.cz + (size_t)g * capc;
+    int32_t* ci = a.ws.ci + (size_t)g * capc;
+    for (int i = base + lane(); i < wend; i += kWave) {
+      cz[i] = cm.sz[i];
+      ci[i] = cm.si[i];
     }
   }
-  const int wend = min(base + wtot, capc);
-  double* cz = a.ws.cz + (size_t)g * capc;
-  int32_t* ci = a.ws.ci + (size_t)g * capc;
-  for (int i = base + lane(); i < wend; i += kWave) {
-    cz[i] = cm.sz[i];
-    ci[i] = cm.si[i];
-  }
-  um = wave_max(um);
+  // every token left out is below theta
   if (lane() == 0) {
     wp->zmax = hi;
-    wp->umax = um;
+    wp->umax = theta;
     wp->end = wend;
     wp->flags = flags;
   }
@@ -506,7 +546,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   load_chunk<TIn, VEC>(x, a.V, c0, tk.v);
   const bool cands = rp.topk || rp.topp;
   if (cands) {  // ordered before use by the first barrier of chunk_candidates
-    for (int b = threadIdx.x; b < kHB; b += kThreads) cm.hcnt[b] = 0u;
+    for (int b = threadIdx.x; b < kHB + 1; b += kThreads) cm.hcnt[b] = 0u;
     if (threadIdx.x == 0) cm.cand_n = 0;
   }
   int flags = 0;
@@ -814,6 +854,9 @@ __device__ __forceinline__ SelOut select_desc(uint32_t act, const RegCands& rc, 
         ++slot;
       }
     wg_barrier();
+    // lane i of every wave holds entry i; wave w compares it with entries
+    // j in [8w, 8w + 8) (LDS broadcast reads) and adds its counts to the
+    // entry's totals
     const int m = uniform((int)cnt);
     const int ln = lane();
     uint64_t k = 0ull, w = 0ull;
@@ -823,15 +866,28 @@ __device__ __forceinline__ SelOut select_desc(uint32_t act, const RegCands& rc, 
       ix = rl.idx[ln];
       w = rl.w[ln];
     }
-    int rank = 0;
+    uint32_t rank = 0;
     uint64_t ahead = 0;
-#pragma unroll 8
-    for (int j = 0; j < m; ++j) {  // every lane reads entry j: LDS broadcast
-      const uint64_t kj = rl.key[j];
-      const int ij = rl.idx[j];
-      const bool bj = kj > k || (kj == k && ij < ix);
-      rank += bj ? 1 : 0;
-      if (MASS) ahead += bj ? rl.w[j] : 0ull;
+    constexpr int kPerWave = kWave / kWaves;
+#pragma unroll
+    for (int jj = 0; jj < kPerWave; ++jj) {
+      const int j = wave() * kPerWave + jj;
+      if (j < m) {
+        const uint64_t kj = rl.key[j];
+        const int ij = rl.idx[j];
+        const bool bj = kj > k || (kj == k && ij < ix);
+        rank += bj ? 1u : 0u;
+        if (MASS) ahead += bj ? rl.w[j] : 0ull;
+      }
+    }
+    if (ln < m) {
+      lds_add(&rl.rank[ln], rank);
+      if (MASS) lds_add(&rl.ahead[ln], ahead);
+    }
+    wg_barrier();
+    if (ln < m) {
+      rank = rl.rank[ln];
+      ahead = rl.ahead[ln];
     }
     bool hit;
     if (!MASS) hit = ln < m && (uint64_t)rank == target - above - 1;
@@ -1189,6 +1245,10 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
     }
     if (threadIdx.x < kDrawSpanMax) fs.dspan[threadIdx.x] = 0ull;
     if (threadIdx.x < 2) fs.rl[threadIdx.x].n = 0;
+    if (threadIdx.x < 2 * kWave) {
+      fs.rl[threadIdx.x / kWave].rank[threadIdx.x % kWave] = 0u;
+      fs.rl[threadIdx.x / kWave].ahead[threadIdx.x % kWave] = 0ull;
+    }
   }
   XWave xw{fs.xw, 0};
   int hgen = 0;
