@@ -773,30 +773,32 @@ struct SelOut {
   int idx;
 };
 
-template <bool MASS, class Key>
-__device__ __forceinline__ SelOut select_desc(uint32_t act, const RegCands& rc, const Key& key, uint64_t target,
+// The order key of slot q is keyf(rc.v[q]), non-decreasing in rc.v[q], so
+// the key range of the active set comes from the range of the values.
+template <bool MASS, class KeyF>
+__device__ __forceinline__ SelOut select_desc(uint32_t act, const RegCands& rc, const KeyF& keyf, uint64_t target,
                                               int V, RankList& rl, FastSmem& fs, XWave& xw, int& hgen) {
-  uint64_t lo = ~0ull, hi = 0ull;
+  auto key = [&](int q) -> uint64_t { return keyf(rc.v[q]); };
+  double vlo = INFINITY, vhi = -INFINITY;
 #pragma unroll
   for (int q = 0; q < kPerT; ++q)
     if ((act >> q) & 1u) {
-      const uint64_t k = key(q);
-      lo = k < lo ? k : lo;
-      hi = k > hi ? k : hi;
+      vlo = fmin(vlo, rc.v[q]);
+      vhi = fmax(vhi, rc.v[q]);
     }
   {
-    const auto s = xw.post(wave_min(lo), wave_max(hi), (uint64_t)wave_sum((uint32_t)__popc(act)));
-    lo = s[0][0];
-    hi = s[1][0];
+    const auto s = xw.post(bits_of(wave_min(vlo)), bits_of(wave_max(vhi)), (uint64_t)wave_sum((uint32_t)__popc(act)));
+    vlo = dbl_of(s[0][0]);
+    vhi = dbl_of(s[1][0]);
     uint64_t n = s[2][0];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) {
-      lo = s[0][w] < lo ? s[0][w] : lo;
-      hi = s[1][w] > hi ? s[1][w] : hi;
+      vlo = fmin(vlo, dbl_of(s[0][w]));
+      vhi = fmax(vhi, dbl_of(s[1][w]));
       n += s[2][w];
     }
-    lo = uniform(lo);
-    hi = uniform(hi);
+    uint64_t lo = uniform(keyf(vlo));
+    uint64_t hi = uniform(keyf(vhi));
     if (n == 0 || (!MASS && n < target)) return SelOut{false, false, 0, 0};
     target = uniform(target);
     uint32_t cnt = (uint32_t)uniform(n);
@@ -1165,7 +1167,7 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, RegCands& r
   // ---- top-k: k-th largest with multiplicity, keep y >= kth_y (:76-78)
   double z_lo = -INFINITY;
   if (TOPK) {
-    const SelOut r = select_desc<false>(rc.valid, rc, [&](int q) { return key_of(rc.v[q]); }, (uint64_t)rp.top_k,
+    const SelOut r = select_desc<false>(rc.valid, rc, [](double z) { return key_of(z); }, (uint64_t)rp.top_k,
                                         V, fs.rl[0], fs, xw, hgen);
     if (!r.found) return FastOut{V - 1, true};
     const double kth_z = val_of_key(r.key);
@@ -1209,7 +1211,7 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, RegCands& r
   // ---- top-p: first token (p desc, index asc) whose inclusive mass reaches
   // top_p (:82-90)
   if (rp.topp) {
-    const SelOut r = select_desc<true>(pos, rc, [&](int q) { return pkey_of(rc.v[q]); }, topp_target(rp.top_p), V,
+    const SelOut r = select_desc<true>(pos, rc, [](double p) { return pkey_of(p); }, topp_target(rp.top_p), V,
                                        fs.rl[1], fs, xw, hgen);
     if (r.giveup) return FastOut{V - 1, true};
     if (r.found) {
