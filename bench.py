@@ -17,6 +17,13 @@ The CPU baseline is the numpy oracle looping over rows like the reference
 engine (llm_engine.py:238-254), one pinned core with BLAS threads pinned to
 1, on a bounded sample of the same workload, in a child process that never
 touches the GPU.
+
+HBM traffic per launch (roofline.traffic) comes from two rocprofv3 counter
+runs of `bench.py --pmc-probe` (FETCH_SIZE, then WRITE_SIZE), each scaled by
+what the same counter reads for a device-to-device copy of known size in
+the same process; `bench.py --traffic-from FETCH_DIR WRITE_DIR` turns the
+two result folders into profiles/traffic_<workload>.json, which later runs
+report.
 """
 
 from __future__ import annotations
@@ -79,6 +86,78 @@ def run_cpu_baseline(workload: str, rows: int, reps: int):
     return json.loads(r.stdout.strip().splitlines()[-1])
 
 
+COPY_BYTES = 256 << 20
+
+
+def pmc_probe(workload: str) -> None:
+    """A short run for counter collection: a copy of COPY_BYTES (the
+    calibration), then a few sampler steps."""
+    import torch
+
+    from pagellm_amd import _native, workloads
+    from pagellm_amd.sampling import _pack_histories, _pack_params
+
+    w = workloads.WORKLOADS[workload]()
+    B, V = w["logits"].shape
+    dev = torch.device("cuda:0")
+    ctx = _native.Context(0)
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    t, k, p, r = _pack_params(w["params"])
+    hist_ids, hist_off = _pack_histories(w["contexts"], w["params"], B, V)
+    x = torch.from_numpy(w["logits"]).to(dev)
+    d = {n: torch.from_numpy(a).to(dev) for n, a in
+         dict(t=t, k=k, p=p, r=r, u=w["uniforms"], ids=hist_ids, off=hist_off).items() if a is not None}
+    out = torch.empty(B, dtype=torch.int32, device=dev)
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        ctx.sample(x.data_ptr(), _native.PLH_F32, V, B, V,
+                   d["ids"].data_ptr() if "ids" in d else None, d["off"].data_ptr() if "off" in d else None,
+                   d["t"].data_ptr(), d["k"].data_ptr(), d["p"].data_ptr(), d["r"].data_ptr(),
+                   d["u"].data_ptr(), out.data_ptr(), None, 0)
+    torch.cuda.synchronize()
+    ctx.close()
+    print("pmc probe done", flush=True)
+
+
+def traffic_from(workload: str, fetch_dir: str, write_dir: str) -> None:
+    """HBM bytes per k_sample_chunks launch from the two counter runs."""
+    import csv
+
+    def per_kernel(folder: str, counter: str):
+        rows = {}
+        for f in Path(folder).rglob("*counter_collection.csv"):
+            for r in csv.DictReader(open(f)):
+                if r["Counter_Name"] != counter:
+                    continue
+                key = (r["Dispatch_Id"], r["Kernel_Name"])
+                rows[key] = rows.get(key, 0.0) + float(r["Counter_Value"])
+        return rows
+
+    res = {}
+    for counter, folder in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        rows = per_kernel(folder, counter)
+        chunks = [v for (_, n), v in rows.items() if "k_sample_chunks" in n]
+        copies = [v for (_, n), v in rows.items() if "copy" in n.lower() or "elementwise" in n.lower()]
+        if not chunks or not copies:
+            raise SystemExit(f"{counter}: no k_sample_chunks or copy dispatch in {folder}")
+        kib_copy = max(copies)
+        factor = COPY_BYTES / (kib_copy * 1024.0)
+        res[counter] = {"kib_per_launch": sum(chunks) / len(chunks), "copy_kib": kib_copy,
+                        "copy_bytes": COPY_BYTES, "scale": factor,
+                        "bytes_per_launch": sum(chunks) / len(chunks) * 1024.0 * factor}
+    from pagellm_amd import workloads
+    w = workloads.WORKLOADS[workload]()
+    out = {"workload": workload, "kernel": "k_sample_chunks",
+           "bytes_per_launch": res["FETCH_SIZE"]["bytes_per_launch"] + res["WRITE_SIZE"]["bytes_per_launch"],
+           "algorithmic_bytes": workloads.algorithmic_bytes(w), "counters": res}
+    dst = ROOT / "profiles" / f"traffic_{workload}.json"
+    dst.write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out))
+
+
 def load_traffic(workload: str):
     f = ROOT / "profiles" / f"traffic_{workload}.json"
     if f.exists():
@@ -100,10 +179,18 @@ def main() -> None:
     ap.add_argument("--cpu-rows", type=int, default=256)
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--cpu-baseline-child", action="store_true")
+    ap.add_argument("--pmc-probe", action="store_true", help="short run for rocprofv3 counter passes")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     args = ap.parse_args()
 
     if args.cpu_baseline_child:
         cpu_baseline_child(args.workload, args.cpu_rows, args.cpu_reps)
+        return
+    if args.traffic_from:
+        traffic_from(args.workload, *args.traffic_from)
+        return
+    if args.pmc_probe:
+        pmc_probe(args.workload)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "

@@ -84,8 +84,8 @@ hipError_t launch_sample_rows(const SampleArgs& a, bool f64, bool vec, hipStream
 // (256-byte aligned), and the two launches.
 size_t fast_ws_bytes(int B, int V, bool f64);
 ChunkWs fast_ws_layout(void* base, int B, int V, bool f64);
-// Aligned rows (vec) stream through num_cu persistent workgroups; `between`,
-// when not null, is recorded on s between the two kernels.
+// `vec`: every row starts 16-byte aligned (16-byte loads); `between`, when
+// not null, is recorded on s between the two kernels.
 hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, int num_cu, hipStream_t s,
                               hipEvent_t between = nullptr);
 hipError_t launch_draw(const DrawArgs& a, bool f64, hipStream_t s);

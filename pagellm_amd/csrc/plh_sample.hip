@@ -10,20 +10,22 @@
 //                      temperature  per-wave segment softmax partials
 //                                   (max, sum of exp);
 //                      top-k/top-p  the chunk's largest tokens (a value
-//                                   histogram picks the threshold) and the
-//                                   largest token left out; top-p-only rows
-//                                   also leave the segment partials.
+//                                   histogram picks the threshold, which
+//                                   also bounds the tokens left out);
+//                                   top-p-only rows also leave the segment
+//                                   partials.
 //                    Every chunk costs one 64 KB read whatever its row's
 //                    mode, and the hardware dispatcher spreads the B x C
 //                    workgroups over the CUs, so mixed batches stay
 //                    balanced.
-//   k_sample_final   one workgroup per row merges the partials: argmax;
-//                    normaliser and the segment holding the inverse-CDF
-//                    point (rescanned with the same arithmetic); or exact
-//                    selection over the gathered candidates (k-th largest,
-//                    top-p cut, fixed-point draw in vocabulary order).  A
-//                    row the candidates cannot decide exactly is finished
-//                    by the general pipeline in the same workgroup.
+//   k_sample_final   one workgroup per row merges the per-wave partials:
+//                    argmax; normaliser and the segment holding the
+//                    inverse-CDF point (rescanned with the same
+//                    arithmetic); or exact selection over the gathered
+//                    candidates (k-th largest, top-p cut, fixed-point draw
+//                    in vocabulary order).  A row the candidates cannot
+//                    decide exactly is finished by the general pipeline in
+//                    the same workgroup.
 // General path:
 //   k_sample_rows    the general pipeline for every row (and the only kernel
 //                    that exports the processed distribution, probs()).
