@@ -40,6 +40,31 @@ __device__ __forceinline__ double fast_exp_neg(double d, const double* tab) {
   return ldexp(tab[k & 63] * q, k >> 6);
 }
 
+// exp(d) for d <= 0 as a term of a normaliser sum: the reduction and
+// polynomial of fast_exp_neg, with k = rint(d * 64 / ln2) from the
+// magic-number rounding (adding 1.5 * 2^52 leaves k in the low mantissa
+// bits) and 2^(k >> 6) added to the exponent field instead of an ldexp.  d
+// is clamped at -708, where the scaled result is still normal: a term
+// below e^-708 (including -inf) counts as e^-708 ~ 3e-308, which no sum
+// holding a term of 1 can notice.
+constexpr double kExpMagic = 6755399441055744.0;  // 1.5 * 2^52
+
+__device__ __forceinline__ double exp_neg_term(double d, const double* tab) {
+  d = fmax(d, -708.0);
+  const double t = fma(d, 64.0 / 0.6931471805599453, kExpMagic);
+  const int k = __double2loint(t);
+  const double kd = t - kExpMagic;
+  double r = fma(-kd, kLn2Hi / 64.0, d);
+  r = fma(-kd, kLn2Lo / 64.0, r);
+  double q = fma(r, 1.0 / 120.0, 1.0 / 24.0);
+  q = fma(q, r, 1.0 / 6.0);
+  q = fma(q, r, 0.5);
+  q = fma(q, r, 1.0);
+  q = fma(q, r, 1.0);
+  const double v = tab[k & 63] * q;
+  return __hiloint2double(__double2hiint(v) + ((k >> 6) << 20), __double2loint(v));
+}
+
 // ------------------------------------------------------- value histograms
 // bin(v) = floor((v - lo) * scale) clamped to [0, nb-1]: monotone
 // non-decreasing in v, so "bin(v) >= d" is a threshold rule on v.

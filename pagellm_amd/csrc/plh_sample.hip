@@ -157,6 +157,15 @@ struct VecOf<double> {
 // with more makes its chunk incomplete (the row takes the general
 // pipeline).
 constexpr int kPenPerWave = 128;
+constexpr uint32_t kCodePen = 0xffffffffu;  // a staged slot written directly (penalised token)
+
+// Raw input values of staged candidates (float32 or float64 bits).
+union StageRaw {
+  float f;
+  double d;
+  __device__ __forceinline__ StageRaw& operator=(float v) { f = v; return *this; }
+  __device__ __forceinline__ StageRaw& operator=(double v) { d = v; return *this; }
+};
 
 // LDS of k_sample_chunks: about 35 KB.
 struct ChunkSmem {
@@ -170,8 +179,10 @@ struct ChunkSmem {
   uint32_t bitmap[Geo<float>::kChunk / 32];
   double pz[kWaves][kPenPerWave];
   int pt[kWaves][kPenPerWave];
-  double sz[kCapChunk];  // candidates staged on their way to the workspace
-  int si[kCapChunk];
+  // candidates staged on their way to the workspace: the raw value and
+  // (lane << 5 | register slot) of the wave that holds it
+  StageRaw sraw[kCapChunk];
+  uint32_t scode[kCapChunk];
   int cand_n;
 };
 
@@ -236,6 +247,9 @@ __device__ __forceinline__ uint32_t chunk_pbits(const SampleArgs& a, const RowPa
   return pb;
 }
 
+// Workgroup min and max in one barrier round.  red is read after the
+// barrier and not released: the caller must not write it again before
+// another barrier.
 __device__ __forceinline__ void block_minmax(double* lo, double* hi, double* red) {
   double a = wave_min(*lo), b = wave_max(*hi);
   if (lane() == 0) {
@@ -250,7 +264,6 @@ __device__ __forceinline__ void block_minmax(double* lo, double* hi, double* red
     a = fmin(a, red[w]);
     b = fmax(b, red[kWaves + w]);
   }
-  wg_barrier();
   *lo = a;
   *hi = b;
 }
@@ -471,17 +484,17 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
   }
   theta = uniform(theta);
   const TIn tin = in_threshold<TIn>(theta);
-  uint32_t pm = 0;
+  int rcnt = 0;  // register tokens kept
   tk.new_pass();
 #pragma unroll
-  for (int e = 0; e < kEpt; ++e) pm |= tk.rv(e) >= tin ? 1u << e : 0u;
+  for (int e = 0; e < kEpt; ++e) rcnt += tk.rv(e) >= tin ? 1 : 0;
   uint32_t qm = 0;  // penalised tokens kept
   for (int i = 0; i < tk.np; ++i) {
     const double z = tk.pen_z(cm, i);
     if (z > -INFINITY && z >= theta) qm |= 1u << i;
   }
   // one LDS reservation per wave (cm.cand_n was reset before the barriers above)
-  const int cnt = __popc(pm) + __popc(qm);
+  const int cnt = rcnt + __popc(qm);
   const int incl = wave_scan_incl(cnt, 0, OpAdd{});
   const int wtot = lane_value(incl, kWave - 1);
   int base = 0;
@@ -495,28 +508,38 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
     flags |= kChunkIncomplete;
     wend = base;
   } else {
+    // register tokens: the raw value and (lane, slot) go to LDS; the
+    // penalised ones (few) straight to the workspace with their float64
+    // value and token id
     int slot = base + incl - cnt;
+    double* cz = a.ws.cz + (size_t)g * capc;
+    int32_t* ci = a.ws.ci + (size_t)g * capc;
+    const uint32_t code0 = (uint32_t)lane() << 5;
     tk.new_pass();
 #pragma unroll
     for (int e = 0; e < kEpt; ++e) {
-      if ((pm >> e) & 1u) {
-        cm.sz[slot] = tk.raw(e);
-        cm.si[slot] = c0 + slot_q<TIn>(e);
+      if (tk.rv(e) >= tin) {
+        cm.sraw[slot] = tk.rv(e);
+        cm.scode[slot] = code0 | (uint32_t)e;
         ++slot;
       }
     }
     for (int i = 0; i < tk.np; ++i) {
       if ((qm >> i) & 1u) {
-        cm.sz[slot] = tk.pen_z(cm, i);
-        cm.si[slot] = tk.pen_tok(cm, i);
+        cm.scode[slot] = kCodePen;
+        cz[slot] = tk.pen_z(cm, i);
+        ci[slot] = tk.pen_tok(cm, i);
         ++slot;
       }
     }
-    double* cz = a.ws.cz + (size_t)g * capc;
-    int32_t* ci = a.ws.ci + (size_t)g * capc;
+    using G = Geo<TIn>;
     for (int i = base + lane(); i < wend; i += kWave) {
-      cz[i] = cm.sz[i];
-      ci[i] = cm.si[i];
+      const uint32_t code = cm.scode[i];
+      if (code != kCodePen) {
+        const int ln = (int)(code >> 5), e = (int)(code & 31u);
+        cz[i] = sizeof(TIn) == 4 ? (double)cm.sraw[i].f : cm.sraw[i].d;
+        ci[i] = c0 + wave() * G::kSeg + (e / G::kVW) * G::kSpan + ln * G::kVW + (e % G::kVW);
+      }
     }
   }
   // every token left out is below theta
@@ -595,8 +618,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     if (m > -INFINITY) {
       tk.new_pass();
 #pragma unroll
-      for (int e = 0; e < G::kEpt; ++e) s += fast_exp_neg(ys(tk.raw(e)) - m, tab);
-      for (int i = 0; i < tk.np; ++i) s += fast_exp_neg(ys(tk.pen_z(cm, i)) - m, tab);
+      for (int e = 0; e < G::kEpt; ++e) s += exp_neg_term(fma(tk.raw(e), ys.invT, -m), tab);
+      for (int i = 0; i < tk.np; ++i) s += exp_neg_term(fma(tk.pen_z(cm, i), ys.invT, -m), tab);
     }
     s = wave_sum(s);
     if (lane() == 0) {
@@ -1101,7 +1124,7 @@ __device__ __forceinline__ int finish_temp(const SampleArgs& a, int row, const R
     if (pos < V) {
       double z = (double)x[pos];
       if (rp.pen_active && ((fs.segbits[(q0 + q) >> 5] >> ((q0 + q) & 31)) & 1u)) z = penalize(z, rp.pen);
-      e[q] = fast_exp_neg(ys(z) - mseg, tab);
+      e[q] = z > -INFINITY ? exp_neg_term(fma(z, ys.invT, -mseg), tab) : 0.0;
     }
     es += e[q];
   }
