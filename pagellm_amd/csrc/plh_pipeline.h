@@ -2,19 +2,23 @@
 //
 // The pipeline restates src/pagellm/engine/sampling.py:65-107 (penalty ->
 // temperature -> top-k -> softmax -> top-p -> inverse-CDF draw, greedy
-// argmax) over an element source; RowSource streams a whole logits row from
-// HBM once per pass.  It is the general path (any parameters, any
-// distribution) and the path that exports the processed distribution.
-// Sorting is replaced by selection: top-k is an MSD radix select by count on
-// order-preserving 64-bit keys of the penalised logits; the top-p cut is an
-// MSD radix select by fixed-point probability mass on the bits of p, in the
-// reference's (p descending, index ascending) order; the draw is an exact
+// argmax) over a logits row streamed from HBM once per pass, 32 consecutive
+// tokens per thread per group with all of a group's loads in flight
+// together.  It is the general path (any parameters, any distribution) and
+// the path that exports the processed distribution.  Sorting is replaced by
+// selection: top-k is an MSD radix select by count on order-preserving
+// 64-bit keys of the penalised logits; the top-p cut is an MSD radix select
+// by fixed-point probability mass on the same keys (p is non-decreasing in
+// z, so (z descending, index ascending) is the reference's (p descending,
+// index ascending) order except where two logits round to one p), which
+// computes p only for the tokens still in play; the draw is an exact
 // integer prefix scan in vocabulary order.
 #pragma once
 
 #include <limits.h>
 
 #include "plh_device.h"
+#include "plh_fast.h"
 
 namespace plh {
 
@@ -35,6 +39,7 @@ struct Smem {
   uint64_t lkey[kSmall];
   uint64_t lw[kSmall];
   int32_t lidx[kSmall];
+  double exp_tab[64];
   uint32_t bitmap[kMaxVBitmap / 32];
 };
 
@@ -62,23 +67,29 @@ __device__ __forceinline__ void build_bitmap(uint32_t* bitmap, int lo, int n, co
   __syncthreads();
 }
 
-// p(z) of the processed distribution for elements that survived top-k
-// (z >= z_lo); sampling.py:75-81.
+// p(z) of the processed distribution for tokens that survived top-k
+// (z >= z_lo); sampling.py:75-81, with y = z * (1 / T) and the table exp.
 struct PCalc {
-  double T, ymax, S, z_lo;
+  double invT, ymax, invS, z_lo;
+  const double* tab;
 };
 
 __device__ __forceinline__ double p_of(const PCalc& c, double z) {
   if (!(z >= c.z_lo)) return 0.0;
-  const double y = (c.T == 1.0) ? z : z / c.T;
-  return exp(y - c.ymax) / c.S;
+  return fast_exp_neg(z * c.invT - c.ymax, c.tab) * c.invS;
 }
 
-// ------------------------------------------------------------ sources
+// ------------------------------------------------------------ source
 
-// Positions base + 4*tid + l (l = 0..3) of a tile of 4*kThreads elements.
+// A logits row, penalised on the fly from an LDS bitmap.  group(base, f)
+// covers tokens [base, base + kGroup): thread t owns the 32 consecutive
+// tokens base + 32t .. base + 32t + 31, loaded before any is used; f(j, z,
+// idx) is called for each of them in order (invalid ones: z = -inf, idx =
+// INT_MAX).
 template <typename TIn, bool VEC>
 struct RowSource {
+  static constexpr int kPer = 32;
+  static constexpr int kGroup = kPer * kThreads;
   const TIn* x;  // row base
   int V;
   const uint32_t* bits;  // LDS penalty bitmap over [0, V)
@@ -87,47 +98,37 @@ struct RowSource {
 
   __device__ __forceinline__ int n() const { return V; }
 
-  __device__ __forceinline__ void load4(int base, double z[4], int idx[4], bool valid[4], int addr[4]) const {
-    const int p0 = base + 4 * (int)threadIdx.x;
-    if (VEC && p0 + 3 < V) {
+  template <class F>
+  __device__ __forceinline__ void group(int base, const F& f) const {
+    const int p0 = base + kPer * (int)threadIdx.x;
+    TIn raw[kPer];
+    if (VEC && p0 + kPer <= V) {
       if constexpr (sizeof(TIn) == 4) {
-        const float4 v = *reinterpret_cast<const float4*>(x + p0);
-        z[0] = v.x; z[1] = v.y; z[2] = v.z; z[3] = v.w;
-      } else {
-        const double2 a = *reinterpret_cast<const double2*>(x + p0);
-        const double2 b = *reinterpret_cast<const double2*>(x + p0 + 2);
-        z[0] = a.x; z[1] = a.y; z[2] = b.x; z[3] = b.y;
-      }
 #pragma unroll
-      for (int l = 0; l < 4; ++l) valid[l] = true;
+        for (int u = 0; u < kPer / 4; ++u) {
+          const float4 v = *reinterpret_cast<const float4*>(x + p0 + 4 * u);
+          raw[4 * u] = v.x; raw[4 * u + 1] = v.y; raw[4 * u + 2] = v.z; raw[4 * u + 3] = v.w;
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < kPer / 2; ++u) {
+          const double2 v = *reinterpret_cast<const double2*>(x + p0 + 2 * u);
+          raw[2 * u] = v.x; raw[2 * u + 1] = v.y;
+        }
+      }
     } else {
 #pragma unroll
-      for (int l = 0; l < 4; ++l) {
-        valid[l] = p0 + l < V;
-        z[l] = valid[l] ? (double)x[p0 + l] : -INFINITY;
-      }
+      for (int j = 0; j < kPer; ++j) raw[j] = p0 + j < V ? x[p0 + j] : (TIn)(-INFINITY);
     }
-    if (pen_on && p0 < V) {
-      const uint32_t w = bits[p0 >> 5] >> (p0 & 31);
+    uint32_t pb = 0u;  // p0 is a multiple of 32: its bits are one word
+    if (pen_on && p0 < V) pb = bits[p0 >> 5];
 #pragma unroll
-      for (int l = 0; l < 4; ++l)
-        if (valid[l] && ((w >> l) & 1u)) z[l] = penalize(z[l], pen);
+    for (int j = 0; j < kPer; ++j) {
+      const bool valid = p0 + j < V;
+      double z = (double)raw[j];
+      if ((pb >> j) & 1u) z = penalize(z, pen);
+      f(j, valid ? z : -INFINITY, valid ? p0 + j : INT_MAX);
     }
-#pragma unroll
-    for (int l = 0; l < 4; ++l) {
-      idx[l] = valid[l] ? p0 + l : INT_MAX;
-      addr[l] = p0 + l;
-    }
-  }
-
-  __device__ __forceinline__ void prepare_p(const PCalc&, Smem&) {}
-
-  __device__ __forceinline__ void load4p(int base, double z[4], int idx[4], bool valid[4], double p[4],
-                                         const PCalc& pc) const {
-    int addr[4];
-    load4(base, z, idx, valid, addr);
-#pragma unroll
-    for (int l = 0; l < 4; ++l) p[l] = valid[l] ? p_of(pc, z[l]) : 0.0;
   }
 };
 
@@ -194,62 +195,11 @@ struct SelResult {
   uint32_t tie_count;
 };
 
-// `visit(fn)` calls fn(key, weight, idx) once for every eligible element the
-// calling thread owns; every thread of the workgroup must call visit.
-//
-// kCount: the target-th largest key (1-based, with multiplicity).
-// kMass:  in (key descending, idx ascending) order, the first element whose
-//         inclusive weight sum reaches target.
-// found == false when the eligible total is below target.
-template <int MODE, class Visit>
-__device__ __forceinline__ SelResult radix_select(const Visit& visit, uint64_t target, Smem& sm) {
-  uint64_t prefix = 0, above = 0;
-  uint32_t bincnt = 0;
-  int done = 0;
-  const int widths[6] = {11, 11, 11, 11, 10, 10};
-  for (int pass = 0; pass < 6; ++pass) {
-    const int w = widths[pass];
-    const int shift = 64 - done - w;
-    const int nb = 1 << w;
-    const uint64_t dmask = (uint64_t)(nb - 1);
-    for (int b = threadIdx.x; b < nb; b += kThreads) {
-      sm.cnt[b] = 0u;
-      if (MODE == kMass) sm.mass[b] = 0ull;
-    }
-    __syncthreads();
-    visit([&](uint64_t key, uint64_t wt, int) {
-      if (done > 0 && (key >> (64 - done)) != prefix) return;
-      const int d = (int)((key >> shift) & dmask);
-      lds_add(&sm.cnt[d], 1u);
-      if (MODE == kMass) lds_add(&sm.mass[d], wt);
-    });
-    __syncthreads();
-    const BinPick bp = pick_bin_desc<MODE == kMass>(sm, nb, above, target);
-    if (!bp.found) return SelResult{false, false, 0, 0, bp.above, 0};
-    above = bp.above;
-    const int dstar = bp.d;
-    bincnt = sm.cnt[dstar];
-    prefix = (prefix << w) | (uint64_t)dstar;
-    done += w;
-    __syncthreads();
-    if (bincnt <= (uint32_t)kSmall) break;
-  }
-  if (bincnt > (uint32_t)kSmall) {  // done == 64: every element of the bin has key == prefix
-    return SelResult{true, true, prefix, -1, above, bincnt};
-  }
-  // Finish: gather the bin into LDS and sort it in (key desc, idx asc) order.
-  if (threadIdx.x == 0) sm.ctl_i[2] = 0;
-  __syncthreads();
-  visit([&](uint64_t key, uint64_t wt, int idx) {
-    if ((key >> (64 - done)) != prefix) return;
-    const int slot = lds_fetch_add(&sm.ctl_i[2], 1);
-    if (slot < kSmall) {
-      sm.lkey[slot] = key;
-      sm.lw[slot] = wt;
-      sm.lidx[slot] = idx;
-    }
-  });
-  __syncthreads();
+// The gathered list (sm.ctl_i[2] entries, at most kSmall) sorted in (key
+// desc, idx asc) order; the result of a selection whose earlier levels put
+// `above` (count or mass) before the list.
+template <int MODE>
+__device__ __forceinline__ SelResult sorted_pick(uint64_t target, uint64_t above, Smem& sm) {
   const int n = min(sm.ctl_i[2], kSmall);
   int N = 2;
   while (N < n) N <<= 1;
@@ -297,9 +247,186 @@ __device__ __forceinline__ SelResult radix_select(const Visit& visit, uint64_t t
     const int pos = min(sm.ctl_i[3], n - 1);
     r.key = sm.lkey[pos];
     r.idx = sm.lidx[pos];
+    // the mass before the result, for the kept total
+    if (i == pos) sm.ctl_u[1] = above + ex;
+    __syncthreads();
+    r.above = sm.ctl_u[1];
   }
   __syncthreads();
   return r;
+}
+
+
+// `visit(fn)` calls fn(key, wfn, idx) once for every eligible element the
+// calling thread owns, where wfn() returns the element's weight (only the
+// kMass passes call it, and only for elements still in play); every thread
+// of the workgroup must call visit.
+//
+// kCount: the target-th largest key (1-based, with multiplicity).
+// kMass:  in (key descending, idx ascending) order, the first element whose
+//         inclusive weight sum reaches target.
+// found == false when the eligible total is below target (above then holds
+// that total).
+template <int MODE, class Visit>
+__device__ __forceinline__ SelResult radix_select(const Visit& visit, uint64_t target, Smem& sm) {
+  uint64_t prefix = 0, above = 0;
+  uint32_t bincnt = 0;
+  int done = 0;
+  const int widths[6] = {11, 11, 11, 11, 10, 10};
+  for (int pass = 0; pass < 6; ++pass) {
+    const int w = widths[pass];
+    const int shift = 64 - done - w;
+    const int nb = 1 << w;
+    const uint64_t dmask = (uint64_t)(nb - 1);
+    for (int b = threadIdx.x; b < nb; b += kThreads) {
+      sm.cnt[b] = 0u;
+      if (MODE == kMass) sm.mass[b] = 0ull;
+    }
+    __syncthreads();
+    visit([&](uint64_t key, auto wfn, int) {
+      if (done > 0 && (key >> (64 - done)) != prefix) return;
+      const int d = (int)((key >> shift) & dmask);
+      lds_add(&sm.cnt[d], 1u);
+      if (MODE == kMass) lds_add(&sm.mass[d], (uint64_t)wfn());
+    });
+    __syncthreads();
+    const BinPick bp = pick_bin_desc<MODE == kMass>(sm, nb, above, target);
+    if (!bp.found) return SelResult{false, false, 0, 0, bp.above, 0};
+    above = bp.above;
+    const int dstar = bp.d;
+    bincnt = sm.cnt[dstar];
+    prefix = (prefix << w) | (uint64_t)dstar;
+    done += w;
+    __syncthreads();
+    if (bincnt <= (uint32_t)kSmall) break;
+  }
+  if (bincnt > (uint32_t)kSmall) {  // done == 64: every element of the bin has key == prefix
+    return SelResult{true, true, prefix, -1, above, bincnt};
+  }
+  // Finish: gather the bin into LDS and sort it in (key desc, idx asc) order.
+  if (threadIdx.x == 0) sm.ctl_i[2] = 0;
+  __syncthreads();
+  visit([&](uint64_t key, auto wfn, int idx) {
+    if ((key >> (64 - done)) != prefix) return;
+    const int slot = lds_fetch_add(&sm.ctl_i[2], 1);
+    if (slot < kSmall) {
+      sm.lkey[slot] = key;
+      sm.lw[slot] = MODE == kMass ? (uint64_t)wfn() : 0ull;
+      sm.lidx[slot] = idx;
+    }
+  });
+  __syncthreads();
+  return sorted_pick<MODE>(target, above, sm);
+}
+
+// Selection in (z descending, idx ascending) order over elements with value
+// z:
+//   kCount: the target-th element (1-based, with multiplicity);
+//   kMass:  the first element whose inclusive weight sum reaches target.
+// `visit(fn)` calls fn(z, wfn, idx) for every eligible element the calling
+// thread owns (wfn() is its weight; only kMass calls it).  The first level
+// bins z affinely over [zlo, zhi] (kBins bins; values outside clamp to the
+// end bins), so the tokens of a smooth distribution spread over many bins
+// instead of the few an exponent-led radix digit would give; later levels
+// bin the exact 64-bit order keys of the elements still in play (kBins bins
+// of 2^sh consecutive keys), until a bin holds at most kSmall elements,
+// which are sorted.  Result keys are order keys (key_of(z)).  found ==
+// false when the eligible total is below target (above then holds that
+// total); ties: more than kSmall elements share one value.
+template <int MODE, class Visit>
+__device__ __forceinline__ SelResult value_select(const Visit& visit, double zlo, double zhi, uint64_t target,
+                                                  Smem& sm) {
+  const Affine af = make_affine(zlo, zhi, kBins);
+  for (int b = threadIdx.x; b < kBins; b += kThreads) {
+    sm.cnt[b] = 0u;
+    if (MODE == kMass) sm.mass[b] = 0ull;
+  }
+  __syncthreads();
+  visit([&](double z, auto wfn, int) {
+    const int d = af.bin(z);
+    lds_add(&sm.cnt[d], 1u);
+    if (MODE == kMass) lds_add(&sm.mass[d], (uint64_t)wfn());
+  });
+  __syncthreads();
+  BinPick bp = pick_bin_desc<MODE == kMass>(sm, kBins, 0, target);
+  if (!bp.found) return SelResult{false, false, 0, 0, bp.above, 0};
+  uint64_t above = bp.above;
+  const int d0 = bp.d;
+  uint32_t bincnt = sm.cnt[d0];
+  __syncthreads();
+  // exact key range [klo, khi] of the elements still in play
+  uint64_t klo = 0, khi = ~0ull;
+  bool keyed = false;
+  auto in_play = [&](double z) -> bool {
+    if (af.bin(z) != d0) return false;
+    if (!keyed) return true;
+    const uint64_t k = key_of(z);
+    return k >= klo && k <= khi;
+  };
+  for (int lev = 0; bincnt > (uint32_t)kSmall; ++lev) {
+    if (!keyed) {
+      uint64_t lo = ~0ull, hi = 0ull;
+      visit([&](double z, auto, int) {
+        if (af.bin(z) != d0) return;
+        const uint64_t k = key_of(z);
+        lo = k < lo ? k : lo;
+        hi = k > hi ? k : hi;
+      });
+      lo = wave_min(lo);
+      hi = wave_max(hi);
+      if (lane() == 0) {
+        sm.redu[wave()] = lo;
+        sm.lkey[wave()] = hi;
+      }
+      __syncthreads();
+      klo = sm.redu[0];
+      khi = sm.lkey[0];
+      for (int w = 1; w < kWaves; ++w) {
+        klo = sm.redu[w] < klo ? sm.redu[w] : klo;
+        khi = sm.lkey[w] > khi ? sm.lkey[w] : khi;
+      }
+      __syncthreads();
+      keyed = true;
+    }
+    if (klo == khi) return SelResult{true, true, klo, -1, above, bincnt};
+    const uint64_t span = khi - klo;
+    const int sh = span < (uint64_t)kBins ? 0 : 64 - __clzll((long long)span) - 11;
+    for (int b = threadIdx.x; b < kBins; b += kThreads) {
+      sm.cnt[b] = 0u;
+      if (MODE == kMass) sm.mass[b] = 0ull;
+    }
+    __syncthreads();
+    visit([&](double z, auto wfn, int) {
+      if (!in_play(z)) return;
+      const int d = (int)((key_of(z) - klo) >> sh);
+      lds_add(&sm.cnt[d], 1u);
+      if (MODE == kMass) lds_add(&sm.mass[d], (uint64_t)wfn());
+    });
+    __syncthreads();
+    bp = pick_bin_desc<MODE == kMass>(sm, kBins, above, target);
+    if (!bp.found) return SelResult{false, false, 0, 0, bp.above, 0};
+    above = bp.above;
+    bincnt = sm.cnt[bp.d];
+    __syncthreads();
+    const uint64_t nlo = klo + ((uint64_t)bp.d << sh);
+    const uint64_t wid = (1ull << sh) - 1;
+    khi = khi - nlo < wid ? khi : nlo + wid;
+    klo = nlo;
+  }
+  // Finish: gather the bin into LDS and sort it in (key desc, idx asc) order.
+  if (threadIdx.x == 0) sm.ctl_i[2] = 0;
+  __syncthreads();
+  visit([&](double z, auto wfn, int idx) {
+    if (!in_play(z)) return;
+    const int slot = lds_fetch_add(&sm.ctl_i[2], 1);
+    if (slot < kSmall) {
+      sm.lkey[slot] = key_of(z);
+      sm.lw[slot] = MODE == kMass ? (uint64_t)wfn() : 0ull;
+      sm.lidx[slot] = idx;
+    }
+  });
+  __syncthreads();
+  return sorted_pick<MODE>(target, above, sm);
 }
 
 // ----------------------------------------------------------------- draw
@@ -357,68 +484,67 @@ __device__ __forceinline__ int draw_weights(const W& wfn, int V, double u, doubl
 // ------------------------------------------------------------- pipeline
 
 struct PipeIn {
-  bool have_max;
+  bool have_max;  // zmax: the row's largest penalised logit
   double zmax;
-  int argmax;
-  bool have_S;
+  bool have_S;    // S: the full normaliser sum(exp(z / T - zmax / T)), no top-k
   double S;
-  bool cand;  // source holds candidates only
-  double U;   // cand: largest z among elements that are not candidates (-inf: none)
-};
-
-struct PipeOut {
-  int id;
-  bool insufficient;  // cand: the candidates cannot decide this row exactly
+  bool have_min;  // zmin: the row's smallest penalised logit (finite)
+  double zmin;
 };
 
 template <class Src>
-__device__ __forceinline__ PipeOut row_pipeline(Src& src, const RowParams& rp, int V, PipeIn in, Smem& sm, double* probs_out) {
+__device__ __forceinline__ int row_pipeline(Src& src, const RowParams& rp, int V, PipeIn in, Smem& sm,
+                                            double* probs_out) {
   const int n = src.n();
-  constexpr int kTile = 4 * kThreads;
-  PipeOut out{V - 1, false};
+  constexpr int kG = Src::kGroup;
+  constexpr int kPer = Src::kPer;
+  if (threadIdx.x < 64) sm.exp_tab[threadIdx.x] = exp2((double)threadIdx.x / 64.0);
+  __syncthreads();
 
-  // ---- max / argmax of the penalised logits (sampling.py:73, :79, :106)
-  double zmax = in.zmax;
-  int argmax = in.argmax;
-  if (!in.have_max) {
+  // ---- max / argmax of the penalised logits (sampling.py:73, :79, :106),
+  // and the smallest finite one (the range of the selection bins)
+  double zmax = in.zmax, zmin = INFINITY;
+  int argmax = 0;
+  const bool need_min = !rp.greedy && (rp.topk || rp.topp);
+  if (!in.have_max || rp.greedy) {
     ArgMax best{-INFINITY, INT_MAX};
-    for (int base = 0; base < n; base += kTile) {
-      double z[4];
-      int idx[4], addr[4];
-      bool valid[4];
-      src.load4(base, z, idx, valid, addr);
-#pragma unroll
-      for (int l = 0; l < 4; ++l)
-        if (valid[l]) best = argmax_merge(best, ArgMax{z[l], idx[l]});
-    }
+    for (int base = 0; base < n; base += kG)
+      src.group(base, [&](int, double z, int idx) {
+        best = argmax_merge(best, ArgMax{z, idx});
+        if (z > -INFINITY) zmin = fmin(zmin, z);
+      });
     best = block_argmax(best, sm.redd, sm.redi);
     zmax = best.v;
     argmax = best.i;
+    if (need_min) zmin = block_min(zmin, sm.redd);
+  } else if (need_min && in.have_min) {
+    zmin = in.zmin;
+  } else if (need_min) {
+    for (int base = 0; base < n; base += kG)
+      src.group(base, [&](int, double z, int) {
+        if (z > -INFINITY) zmin = fmin(zmin, z);
+      });
+    zmin = block_min(zmin, sm.redd);
   }
   if (rp.greedy) {  // sampling.py:71-74 / :102-106: no temperature, no uniform
-    out.id = argmax;
     if (probs_out != nullptr)
       for (int i = threadIdx.x; i < V; i += kThreads) probs_out[i] = (i == argmax) ? 1.0 : 0.0;
-    return out;
+    return argmax;
   }
   const double T = rp.T;
-  const double ymax = (T == 1.0) ? zmax : zmax / T;
+  const double invT = 1.0 / T;
+  const double ymax = zmax * invT;
 
   // ---- top-k: kth = k-th largest (with multiplicity); keep y >= kth_y (:76-78)
   double z_lo = -INFINITY;
   if (rp.topk) {
     auto visit = [&](auto fn) {
-      for (int base = 0; base < n; base += kTile) {
-        double z[4];
-        int idx[4], addr[4];
-        bool valid[4];
-        src.load4(base, z, idx, valid, addr);
-#pragma unroll
-        for (int l = 0; l < 4; ++l)
-          if (valid[l]) fn(key_of(z[l]), 0ull, idx[l]);
-      }
+      for (int base = 0; base < n; base += kG)
+        src.group(base, [&](int, double z, int idx) {
+          if (idx != INT_MAX) fn(z, [] { return 0ull; }, idx);
+        });
     };
-    const SelResult r = radix_select<kCount>(visit, (uint64_t)rp.top_k, sm);
+    const SelResult r = value_select<kCount>(visit, zmin, zmax, (uint64_t)rp.top_k, sm);
     const double kth_z = val_of_key(r.key);
     if (kth_z > -INFINITY) {
       const double kth_y = (T == 1.0) ? kth_z : kth_z / T;
@@ -431,174 +557,139 @@ __device__ __forceinline__ PipeOut row_pipeline(Src& src, const RowParams& rp, i
         if (yp >= kth_y) z_lo = zp; else break;
       }
     }
-    if (in.cand && !(in.U < z_lo)) {
-      out.insufficient = true;
-      return out;
-    }
   }
 
   // ---- softmax normaliser over the survivors (:79-81)
   double S = in.S;
   if (!in.have_S || rp.topk) {
-    const PCalc pc0{T, ymax, 1.0, z_lo};
+    const PCalc pc0{invT, ymax, 1.0, z_lo, sm.exp_tab};
     double s = 0.0;
-    for (int base = 0; base < n; base += kTile) {
-      double z[4];
-      int idx[4], addr[4];
-      bool valid[4];
-      src.load4(base, z, idx, valid, addr);
-#pragma unroll
-      for (int l = 0; l < 4; ++l)
-        if (valid[l]) s += p_of(pc0, z[l]);
-    }
+    for (int base = 0; base < n; base += kG)
+      src.group(base, [&](int, double z, int idx) {
+        if (idx != INT_MAX) s += p_of(pc0, z);
+      });
     S = block_sum(s, sm.redd);
   }
-  const PCalc pc{T, ymax, S, z_lo};
-  src.prepare_p(pc, sm);
+  const PCalc pc{invT, ymax, 1.0 / S, z_lo, sm.exp_tab};
+  auto wt_of = [&](double z) -> uint64_t { return to_fx(p_of(pc, z)); };
 
-  // ---- top-p: cut at the first token whose inclusive mass reaches top_p (:82-90)
+  // ---- top-p: cut at the first token whose inclusive mass reaches top_p
+  // (:82-90), selected on the logit keys
   bool have_cut = false;
   uint64_t cut_key = 0;
   int cut_idx = INT_MAX;
+  uint64_t kept_tot = 0;  // fixed-point mass of the kept set, when known
+  bool have_tot = false;
   if (rp.topp) {
     const uint64_t target = topp_target(rp.top_p);
+    // tokens below z_lo (outside top-k) weigh nothing and never reach the cut
     auto visit = [&](auto fn) {
-      for (int base = 0; base < n; base += kTile) {
-        double z[4], p[4];
-        int idx[4];
-        bool valid[4];
-        src.load4p(base, z, idx, valid, p, pc);
-#pragma unroll
-        for (int l = 0; l < 4; ++l)
-          if (valid[l]) fn(pkey_of(p[l]), to_fx(p[l]), idx[l]);
-      }
+      for (int base = 0; base < n; base += kG)
+        src.group(base, [&](int, double z, int idx) {
+          if (idx != INT_MAX && z >= z_lo) fn(z, [&] { return wt_of(z); }, idx);
+        });
     };
-    const SelResult r = radix_select<kMass>(visit, target, sm);
-    if (r.found) {
+    const SelResult r = value_select<kMass>(visit, rp.topk ? z_lo : zmin, zmax, target, sm);
+    if (!r.found) {
+      kept_tot = r.above;  // every token is kept
+      have_tot = true;
+    } else {
       have_cut = true;
       cut_key = r.key;
       cut_idx = r.idx;
+      const uint64_t w1 = wt_of(val_of_key(r.key));
+      kept_tot = r.above + w1;
+      have_tot = true;
       if (r.ties) {
-        // r.tie_count tokens share probability key r.key; keep the lowest
-        // indices while the mass before them stays below top_p
-        const uint64_t w1 = to_fx(__longlong_as_double((long long)r.key));
+        // r.tie_count tokens share key r.key; keep the lowest indices while
+        // the mass before them stays below top_p
         uint64_t J = r.tie_count;
         if (w1 > 0) {
           const uint64_t need = (target - r.above - 1) / w1 + 1;
           J = need < J ? need : J;
         }
+        kept_tot = r.above + J * w1;
         if (J >= r.tie_count) {
           cut_idx = INT_MAX;
         } else {
           const uint64_t tkey = r.key;
           auto vis2 = [&](auto fn) {
-            for (int base = 0; base < n; base += kTile) {
-              double z[4], p[4];
-              int idx[4];
-              bool valid[4];
-              src.load4p(base, z, idx, valid, p, pc);
-#pragma unroll
-              for (int l = 0; l < 4; ++l)
-                if (valid[l] && pkey_of(p[l]) == tkey) fn((uint64_t)(0x7fffffff - idx[l]), 0ull, idx[l]);
-            }
+            for (int base = 0; base < n; base += kG)
+              src.group(base, [&](int, double z, int idx) {
+                if (idx != INT_MAX && key_of(z) == tkey) fn((uint64_t)(0x7fffffff - idx), [] { return 0ull; }, idx);
+              });
           };
           const SelResult r2 = radix_select<kCount>(vis2, J, sm);
           cut_idx = 0x7fffffff - (int)r2.key;
         }
       }
     }
-    if (in.cand && !rp.topk && in.U > -INFINITY) {
-      const double pU = p_of(pc, in.U);
-      if (!(have_cut && cut_key > pkey_of(pU))) {
-        out.insufficient = true;
-        return out;
-      }
-    }
   }
 
   // a token survives top-p when it precedes or is the cut token in
-  // (p descending, index ascending) order
-  auto kept = [&](double p, int idx) -> bool {
-    if (!(p > 0.0)) return false;
+  // (z descending, index ascending) order
+  auto kept = [&](double z, int idx) -> bool {
+    if (idx == INT_MAX || !(z >= z_lo)) return false;
     if (!have_cut) return true;
-    const uint64_t k = pkey_of(p);
+    const uint64_t k = key_of(z);
     return k > cut_key || (k == cut_key && idx <= cut_idx);
   };
-  auto weight = [&](double p, int idx) -> uint64_t { return kept(p, idx) ? to_fx(p) : 0ull; };
+  auto weight = [&](double z, int idx) -> uint64_t { return kept(z, idx) ? wt_of(z) : 0ull; };
 
   // ---- inverse-CDF draw in vocabulary order (:94-98)
-  uint64_t tot = 0;
-  for (int base = 0; base < n; base += kTile) {
-    double z[4], p[4];
-    int idx[4];
-    bool valid[4];
-    src.load4p(base, z, idx, valid, p, pc);
-#pragma unroll
-    for (int l = 0; l < 4; ++l)
-      if (valid[l]) tot += weight(p[l], idx[l]);
+  if (!have_tot) {
+    uint64_t tot = 0;
+    for (int base = 0; base < n; base += kG)
+      src.group(base, [&](int, double z, int idx) { tot += weight(z, idx); });
+    kept_tot = block_sum<uint64_t>(tot, sm.redu);
   }
-  tot = block_sum<uint64_t>(tot, sm.redu);
-  const uint64_t t_fx = (uint64_t)__double2ull_rd(rp.u * (double)tot);
+  const uint64_t t_fx = (uint64_t)__double2ull_rd(rp.u * (double)kept_tot);
   uint64_t run = 0;
   int found = INT_MAX;
-  for (int base = 0; base < n; base += kTile) {
-    double z[4], p[4];
-    int idx[4];
-    bool valid[4];
-    src.load4p(base, z, idx, valid, p, pc);
-    uint64_t w[4], s = 0;
-#pragma unroll
-    for (int l = 0; l < 4; ++l) {
-      w[l] = valid[l] ? weight(p[l], idx[l]) : 0ull;
-      s += w[l];
-    }
-    uint64_t tile_tot;
-    const uint64_t ex = block_excl_scan<uint64_t>(s, sm.redu, &tile_tot);
-    if (run + tile_tot > t_fx) {
+  for (int base = 0; base < n; base += kG) {
+    uint64_t w[kPer], s = 0;
+    int ix[kPer];
+    src.group(base, [&](int j, double z, int idx) {
+      w[j] = weight(z, idx);
+      ix[j] = idx;
+      s += w[j];
+    });
+    uint64_t group_tot;
+    const uint64_t ex = block_excl_scan<uint64_t>(s, sm.redu, &group_tot);
+    if (run + group_tot > t_fx) {
       uint64_t c = run + ex;
       int my = INT_MAX;
 #pragma unroll
-      for (int l = 0; l < 4; ++l) {
-        c += w[l];
-        if (my == INT_MAX && c > t_fx) my = idx[l];
+      for (int j = 0; j < kPer; ++j) {
+        c += w[j];
+        if (my == INT_MAX && c > t_fx) my = ix[j];
       }
       found = block_min<int>(my, sm.redi);
       break;
     }
-    run += tile_tot;
+    run += group_tot;
   }
-  out.id = (found == INT_MAX) ? V - 1 : found;
+  const int id = (found == INT_MAX) ? V - 1 : found;
 
   // ---- optional export of the processed distribution (probs())
   if (probs_out != nullptr) {
     double s2 = 1.0;
     if (have_cut) {
       double s = 0.0;
-      for (int base = 0; base < n; base += kTile) {
-        double z[4], p[4];
-        int idx[4];
-        bool valid[4];
-        src.load4p(base, z, idx, valid, p, pc);
-#pragma unroll
-        for (int l = 0; l < 4; ++l)
-          if (valid[l] && kept(p[l], idx[l])) s += p[l];
-      }
+      for (int base = 0; base < n; base += kG)
+        src.group(base, [&](int, double z, int idx) {
+          if (kept(z, idx)) s += p_of(pc, z);
+        });
       s2 = block_sum(s, sm.redd);
     }
-    for (int base = 0; base < n; base += kTile) {
-      double z[4], p[4];
-      int idx[4];
-      bool valid[4];
-      src.load4p(base, z, idx, valid, p, pc);
-#pragma unroll
-      for (int l = 0; l < 4; ++l) {
-        if (!valid[l]) continue;
+    for (int base = 0; base < n; base += kG)
+      src.group(base, [&](int, double z, int idx) {
+        if (idx == INT_MAX) return;
         // top-p renormalises the kept mass (:89-90); without top-p p is final
-        probs_out[idx[l]] = have_cut ? (kept(p[l], idx[l]) ? p[l] / s2 : 0.0) : p[l];
-      }
-    }
+        probs_out[idx] = have_cut ? (kept(z, idx) ? p_of(pc, z) / s2 : 0.0) : p_of(pc, z);
+      });
   }
-  return out;
+  return id;
 }
 
 }  // namespace plh

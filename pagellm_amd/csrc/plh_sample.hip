@@ -113,12 +113,11 @@ __device__ __forceinline__ RowParams load_row_params(const SampleArgs& a, int ro
 
 template <typename TIn, bool VEC>
 __device__ __forceinline__ int row_general(const SampleArgs& a, int row, const RowParams& rp, Smem& sm,
-                                           double* probs_out) {
+                                           double* probs_out, PipeIn in = PipeIn{false, 0.0, false, 0.0, false, 0.0}) {
   const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
   if (rp.pen_active) build_bitmap(sm.bitmap, 0, a.V, a.hist_ids, rp.h0, rp.h1);
   RowSource<TIn, VEC> src{x, a.V, sm.bitmap, rp.pen_active, rp.pen};
-  const PipeIn in{false, 0.0, 0, false, 0.0, false, -INFINITY};
-  return row_pipeline(src, rp, a.V, in, sm, probs_out).id;
+  return row_pipeline(src, rp, a.V, in, sm, probs_out);
 }
 
 template <typename TIn, bool VEC>
@@ -605,7 +604,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   TIn lm = (TIn)(-INFINITY);
   tk.new_pass();
 #pragma unroll
-  for (int e = 0; e < G::kEpt; ++e) lm = fmax(lm, tk.rv(e));
+  for (int e = 0; e < G::kEpt; ++e) {
+    lm = fmax(lm, tk.rv(e));
+  }
   double lmax = (double)lm;
   for (int i = 0; i < tk.np; ++i) lmax = fmax(lmax, tk.pen_z(cm, i));
   if (cands) chunk_candidates<TIn>(tk, lmax, a, rp, g, c0, flags, wp, cm);
@@ -1146,6 +1147,7 @@ __device__ __forceinline__ int finish_temp(const SampleArgs& a, int row, const R
 struct FastOut {
   int id;
   bool general;  // the candidates cannot decide the row exactly
+  double S;      // general: the full normaliser when known (top-p-only rows), else 0
 };
 
 // Top-k and/or top-p rows (sampling.py:75-90, :94-98) from the gathered
@@ -1194,7 +1196,7 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, RegCands& r
   if (TOPK) {
     const SelOut r = select_desc<false>(rc.valid, rc, [](double z) { return key_of(z); }, (uint64_t)rp.top_k,
                                         V, fs.rl[0], fs, xw, hgen);
-    if (!r.found) return FastOut{V - 1, true};
+    if (!r.found) return FastOut{V - 1, true, 0.0};
     const double kth_z = val_of_key(r.key);
     const double kth_y = yexact(kth_z);
     z_lo = kth_z;
@@ -1203,7 +1205,7 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, RegCands& r
       if (yexact(zp) >= kth_y) z_lo = zp;
       else break;
     }
-    if (!(ps.umax < z_lo)) return FastOut{V - 1, true};
+    if (!(ps.umax < z_lo)) return FastOut{V - 1, true, 0.0};
   }
 
   // ---- softmax (:79-81): p = exp(y - ymax) / S, once per candidate
@@ -1238,7 +1240,7 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, RegCands& r
   if (rp.topp) {
     const SelOut r = select_desc<true>(pos, rc, [](double p) { return pkey_of(p); }, topp_target(rp.top_p), V,
                                        fs.rl[1], fs, xw, hgen);
-    if (r.giveup) return FastOut{V - 1, true};
+    if (r.giveup) return FastOut{V - 1, true, TOPK ? 0.0 : S};
     if (r.found) {
 #pragma unroll
       for (int q = 0; q < kPerT; ++q) {
@@ -1249,12 +1251,12 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, RegCands& r
     if (!TOPK && ps.umax > -INFINITY) {
       // the largest token left out must fall outside the nucleus
       const double pU = fast_exp_neg(ys(ps.umax) - ymax, tab) * invS;
-      if (!(r.found && r.key > pkey_of(pU))) return FastOut{V - 1, true};
+      if (!(r.found && r.key > pkey_of(pU))) return FastOut{V - 1, true, S};
     }
   }
 
   // ---- draw in vocabulary order (:94-98)
-  return FastOut{draw_kept(rc, V, rp.u, fs, hgen), false};
+  return FastOut{draw_kept(rc, V, rp.u, fs, hgen), false, 0.0};
 }
 
 template <typename TIn, bool VEC>
@@ -1291,6 +1293,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   // row to the general pipeline
   bool general = ps.flags != 0;
   int id = 0;
+  PipeIn pin{false, 0.0, false, 0.0, false, 0.0};  // what the fast path already knows of the row
   if (general) {
   } else if (rp.greedy) {
     id = ps.best.i;
@@ -1301,11 +1304,12 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
                               : finish_cands<TIn, false>(a, rc, sg, rp, ps, fs, xw, hgen);
     id = o.id;
     general = o.general;
+    pin = PipeIn{true, ps.zmax, o.S > 0.0, o.S, false, 0.0};
   }
   if (general) {
     wg_barrier();
     if (threadIdx.x == 0) glb_add(a.fallback_rows, 1ull);
-    id = row_general<TIn, VEC>(a, row, rp, sm.g, nullptr);
+    id = row_general<TIn, VEC>(a, row, rp, sm.g, nullptr, pin);
   }
   if (threadIdx.x == 0) a.out_ids[row] = id;
 }
