@@ -43,6 +43,10 @@ extern "C" {
 
 /* plh_sample flags */
 #define PLH_SAMPLE_ROWWISE 1 /* one workgroup per row (the general kernel) */
+#define PLH_SAMPLE_HIST_SPANS 2 /* hist_off holds B (start, end) pairs into
+                                   hist_ids instead of B+1 CSR offsets, so
+                                   histories can live in fixed per-sequence
+                                   slots that grow in place (plh_append_ids) */
 
 /* plh_set_option options */
 #define PLH_OPT_KERNEL_TIMING 1 /* value 1: bracket the fast path's kernels with
@@ -89,7 +93,9 @@ int plh_sync(plh_ctx* ctx);
  *   logits      [B, ld] of `dtype` (PLH_F32 / PLH_F64); row b starts at b*ld
  *   hist_ids    int32 token ids, CSR over rows (the sequence's full history,
  *               prompt + outputs, llm_engine.py:283); may be NULL with
- *   hist_off    int64 [B+1] offsets into hist_ids, or NULL (no history)
+ *   hist_off    int64 [B+1] offsets into hist_ids, or NULL (no history);
+ *               with PLH_SAMPLE_HIST_SPANS, int64 [2B]: row b's history is
+ *               hist_ids[hist_off[2b] .. hist_off[2b+1])
  *   temperature float64 [B]  0 => greedy (SamplingParams.greedy, :47-49)
  *   top_k       int32 [B]    0 or >= V => disabled
  *   top_p       float64 [B]  1 => disabled
@@ -141,6 +147,25 @@ int plh_draw(plh_ctx* ctx, const void* p, int dtype, int64_t ld, int B, int V,
 int plh_verify(plh_ctx* ctx, const void* p, const void* q, int dtype, int B, int k, int V,
                const int32_t* draft, const double* accept_u, const double* draw_u,
                int draw_u_per_stop, int32_t* out_tokens, int32_t* out_n_acc);
+
+/*
+ * Strided device-to-device copy on the context's stream: rows x row_bytes
+ * from src (pitch src_pitch bytes) to dst (pitch dst_pitch bytes).  Places
+ * a [B, V] block (for instance draft distributions exported by plh_sample)
+ * at one position of a [B, k, V] buffer for plh_verify.  No counterpart in
+ * the reference (host lists play this role there).
+ */
+int plh_copy_rows(plh_ctx* ctx, void* dst, int64_t dst_pitch, const void* src, int64_t src_pitch,
+                  int64_t row_bytes, int rows);
+
+/*
+ * Appends sampled ids to device-resident histories: the step of
+ * src/pagellm/engine/llm_engine.py:284 (seq.tokens.append(tok)) for a batch,
+ * without a host round trip.  slab[pos[i]] = ids[i] for i < n; entries with
+ * pos[i] < 0 are skipped.  slab, pos (int64 [n]) and ids (int32 [n], e.g.
+ * plh_sample's out_ids) are device pointers; ordered on the context's stream.
+ */
+int plh_append_ids(plh_ctx* ctx, int32_t* slab, const int64_t* pos, const int32_t* ids, int n);
 
 #ifdef __cplusplus
 }

@@ -25,6 +25,7 @@ PLH_ERR_NO_DEVICE = -5
 PLH_F32 = 0
 PLH_F64 = 1
 PLH_SAMPLE_ROWWISE = 1
+PLH_SAMPLE_HIST_SPANS = 2
 PLH_OPT_KERNEL_TIMING = 1
 
 _c_int, _c_i64, _c_sz, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
@@ -55,6 +56,8 @@ SIGNATURES = {
         _c_int,
         [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp],
     ),
+    "plh_append_ids": (_c_int, [_vp, _vp, _vp, _vp, _c_int]),
+    "plh_copy_rows": (_c_int, [_vp, _vp, _c_i64, _vp, _c_i64, _c_i64, _c_int]),
 }
 
 _lib = None
@@ -240,6 +243,13 @@ class Context:
             self.lib.plh_penalize(self.handle, x_ptr, dtype_code, ld, B, V, hist_ids, hist_off, rep_penalty,
                                   out_ptr, out_ld)
         )
+
+    def copy_rows(self, dst_ptr, dst_pitch, src_ptr, src_pitch, row_bytes, rows) -> None:
+        self._check(self.lib.plh_copy_rows(self.handle, dst_ptr, int(dst_pitch), src_ptr, int(src_pitch),
+                                           int(row_bytes), int(rows)))
+
+    def append_ids(self, slab_ptr, pos_ptr, ids_ptr, n) -> None:
+        self._check(self.lib.plh_append_ids(self.handle, slab_ptr, pos_ptr, ids_ptr, int(n)))
 
     def draw(self, p_ptr, dtype_code, ld, B, V, uniforms, out_ids) -> None:
         self._check(self.lib.plh_draw(self.handle, p_ptr, dtype_code, ld, B, V, uniforms, out_ids))

@@ -265,6 +265,7 @@ int plh_sample(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, int
   a.V = V;
   a.hist_ids = hist_ids;
   a.hist_off = hist_off;
+  a.hist_spans = (flags & PLH_SAMPLE_HIST_SPANS) ? 1 : 0;
   a.temperature = temperature;
   a.top_k = top_k;
   a.top_p = top_p;
@@ -357,6 +358,33 @@ int plh_verify(plh_ctx* c, const void* p, const void* q, int dtype, int B, int k
   plh::VerifyArgs a{p, q, B, k, V, draft, accept_u, draw_u, draw_u_per_stop ? 1 : 0, out_tokens, out_n_acc};
   const hipError_t e = plh::launch_verify(a, dtype == PLH_F64, c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "plh_verify launch");
+  return PLH_OK;
+}
+
+int plh_copy_rows(plh_ctx* c, void* dst, int64_t dst_pitch, const void* src, int64_t src_pitch, int64_t row_bytes,
+                  int rows) {
+  if (c == nullptr) return PLH_ERR_INVALID_ARG;
+  if (rows < 0 || row_bytes < 0 || dst_pitch < row_bytes || src_pitch < row_bytes)
+    return fail(c, PLH_ERR_INVALID_ARG, "need rows, row_bytes >= 0 and pitches >= row_bytes%s");
+  if (rows == 0 || row_bytes == 0) return PLH_OK;
+  if (dst == nullptr || src == nullptr) return fail(c, PLH_ERR_INVALID_ARG, "null device pointer%s");
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  PLH_HIP(c, hipMemcpy2DAsync(dst, (size_t)dst_pitch, src, (size_t)src_pitch, (size_t)row_bytes, (size_t)rows,
+                              hipMemcpyDeviceToDevice, c->stream),
+          "hipMemcpy2DAsync");
+  return PLH_OK;
+}
+
+int plh_append_ids(plh_ctx* c, int32_t* slab, const int64_t* pos, const int32_t* ids, int n) {
+  if (c == nullptr) return PLH_ERR_INVALID_ARG;
+  if (n < 0) return fail(c, PLH_ERR_INVALID_ARG, "need n >= 0%s");
+  if (n == 0) return PLH_OK;
+  if (slab == nullptr || pos == nullptr || ids == nullptr) return fail(c, PLH_ERR_INVALID_ARG, "null device pointer%s");
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  const hipError_t e = plh::launch_append(slab, pos, ids, n, c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "plh_append_ids launch");
   return PLH_OK;
 }
 

@@ -36,7 +36,8 @@ struct SampleArgs {
   int64_t ld;
   int B, V;
   const int32_t* hist_ids;
-  const int64_t* hist_off;
+  const int64_t* hist_off;  // B+1 CSR offsets, or B (start, end) pairs
+  int hist_spans;           // 1: hist_off holds (start, end) pairs
   const double* temperature;
   const int32_t* top_k;
   const double* top_p;
@@ -91,5 +92,6 @@ hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, int num_c
 hipError_t launch_draw(const DrawArgs& a, bool f64, hipStream_t s);
 hipError_t launch_penalize(const PenalizeArgs& a, bool f64, hipStream_t s);
 hipError_t launch_verify(const VerifyArgs& a, bool f64, hipStream_t s);
+hipError_t launch_append(int32_t* slab, const int64_t* pos, const int32_t* ids, int n, hipStream_t s);
 
 }  // namespace plh

@@ -101,8 +101,8 @@ __device__ __forceinline__ RowParams load_row_params(const SampleArgs& a, int ro
   rp.top_p = a.top_p[row];
   rp.pen = a.rep_penalty[row];
   rp.u = a.uniforms != nullptr ? a.uniforms[row] : 0.0;
-  rp.h0 = a.hist_off != nullptr ? a.hist_off[row] : 0;
-  rp.h1 = a.hist_off != nullptr ? a.hist_off[row + 1] : 0;
+  rp.h0 = a.hist_off != nullptr ? a.hist_off[a.hist_spans ? 2 * row : row] : 0;
+  rp.h1 = a.hist_off != nullptr ? a.hist_off[a.hist_spans ? 2 * row + 1 : row + 1] : 0;
   rp.greedy = rp.T == 0.0;  // SamplingParams.greedy (sampling.py:47-49)
   // sampling.py:56: no penalty when it is 1.0 or the context is empty
   rp.pen_active = rp.pen != 1.0 && rp.h1 > rp.h0 && a.hist_ids != nullptr;
@@ -1357,6 +1357,18 @@ __global__ __launch_bounds__(kThreads) void k_penalize(PenalizeArgs a) {
   }
 }
 
+// ----------------------------------------------------------------- append
+
+// slab[pos[i]] = ids[i] (pos[i] >= 0): the sampled ids join their
+// sequences' device-resident histories (llm_engine.py:284).
+__global__ __launch_bounds__(256) void k_append(int32_t* slab, const int64_t* pos, const int32_t* ids, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) {
+    const int64_t q = pos[i];
+    if (q >= 0) slab[q] = ids[i];
+  }
+}
+
 // ---------------------------------------------------------------- launch
 
 namespace {
@@ -1431,6 +1443,11 @@ hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, int num_c
   auto final_ = f64 ? (vec ? k_sample_final<double, true> : k_sample_final<double, false>)
                     : (vec ? k_sample_final<float, true> : k_sample_final<float, false>);
   hipLaunchKernelGGL(final_, gf, block, 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_append(int32_t* slab, const int64_t* pos, const int32_t* ids, int n, hipStream_t s) {
+  hipLaunchKernelGGL(k_append, dim3((n + 255) / 256), dim3(256), 0, s, slab, pos, ids, n);
   return hipGetLastError();
 }
 

@@ -59,7 +59,8 @@ def test_status_codes_match_header():
 
     text = HEADER.read_text()
     for name in ["PLH_OK", "PLH_ERR_INVALID_ARG", "PLH_ERR_HIP", "PLH_ERR_OUT_OF_MEMORY", "PLH_ERR_UNSUPPORTED",
-                 "PLH_ERR_NO_DEVICE", "PLH_F32", "PLH_F64", "PLH_SAMPLE_ROWWISE", "PLH_OPT_KERNEL_TIMING"]:
+                 "PLH_ERR_NO_DEVICE", "PLH_F32", "PLH_F64", "PLH_SAMPLE_ROWWISE", "PLH_SAMPLE_HIST_SPANS",
+                 "PLH_OPT_KERNEL_TIMING"]:
         m = re.search(rf"#define {name} (-?\d+)", text)
         assert m and int(m.group(1)) == getattr(_native, name), name
 
@@ -72,6 +73,8 @@ def test_null_context_is_an_invalid_argument(lib):
     assert lib.plh_sync(None) == -1
     assert lib.plh_set_option(None, 1, 1) == -1
     assert lib.plh_kernel_times(None, None, None, None) == -1
+    assert lib.plh_append_ids(None, None, None, None, 1) == -1
+    assert lib.plh_copy_rows(None, None, 8, None, 8, 8, 1) == -1
     assert lib.plh_last_error(None) == b"null context"
     lib.plh_destroy(None)
 
