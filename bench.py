@@ -158,6 +158,102 @@ def traffic_from(workload: str, fetch_dir: str, write_dir: str) -> None:
     print(json.dumps(out))
 
 
+def bench_config(name: str, steps: int = 20, warmup: int = 3) -> dict:
+    """rows/s of one more sampling workload, inputs resident in HBM (two
+    rotating copies of the logits), timed with HIP events like the headline."""
+    import torch
+
+    from pagellm_amd import _native, workloads
+    from pagellm_amd.sampling import _pack_histories, _pack_params
+
+    w = workloads.WORKLOADS[name]()
+    B, V = w["logits"].shape
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)
+    ctx = _native.Context(0)
+    ctx.set_stream(stream.cuda_stream)
+    t, k, p, r = _pack_params(w["params"])
+    hist_ids, hist_off = _pack_histories(w["contexts"], w["params"], B, V)
+    xs = [torch.from_numpy(w["logits"]).to(dev) for _ in range(2)]
+    d = {n: torch.from_numpy(a).to(dev) for n, a in
+         dict(t=t, k=k, p=p, r=r, u=w["uniforms"], ids=hist_ids, off=hist_off).items() if a is not None}
+    out = torch.empty(B, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+
+    def step(i):
+        ctx.sample(xs[i % 2].data_ptr(), _native.PLH_F32, V, B, V,
+                   d["ids"].data_ptr() if "ids" in d else None, d["off"].data_ptr() if "off" in d else None,
+                   d["t"].data_ptr(), d["k"].data_ptr(), d["p"].data_ptr(), d["r"].data_ptr(),
+                   d["u"].data_ptr(), out.data_ptr(), None, 0)
+
+    fb0 = ctx.fallback_rows()
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            step(i)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for i in range(steps):
+            step(i)
+        b.record(stream)
+        torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    nbytes = workloads.algorithmic_bytes(w)
+    res = {"rows_per_s": B / (ms * 1e-3), "ms_per_step": ms, "batch": B, "vocab": V,
+           "algorithmic_bytes_per_step": nbytes, "hbm_gbps": nbytes / (ms * 1e-3) / 1e9,
+           "fallback_rows_per_step": (ctx.fallback_rows() - fb0) / (warmup + steps)}
+    ctx.close()
+    return res
+
+
+def bench_verify(steps: int = 50, warmup: int = 5) -> dict:
+    """The speculative verify workload (64 rows, k = 4, V = 32000, float64 p
+    and q resident in HBM): rows/s and the data-dependent compulsory bytes
+    (per row: 16 B per accept test, then the rows the final draw reads:
+    p and q of the rejected position, or p_k)."""
+    import torch
+
+    from pagellm_amd import _native, workloads
+
+    w = workloads.spec32k()
+    B, k1, V = w["p"].shape
+    k = k1 - 1
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)
+    ctx = _native.Context(0)
+    ctx.set_stream(stream.cuda_stream)
+    p = torch.from_numpy(w["p"]).to(dev)
+    q = torch.from_numpy(w["q"]).to(dev)
+    dr = torch.from_numpy(w["draft"].astype("int32")).to(dev)
+    au = torch.from_numpy(w["accept_u"]).to(dev)
+    ru = torch.from_numpy(w["resample_u"]).to(dev)
+    tok = torch.empty((B, k1), dtype=torch.int32, device=dev)
+    nacc = torch.empty(B, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+
+    def step():
+        ctx.verify(p.data_ptr(), q.data_ptr(), _native.PLH_F64, B, k, V, dr.data_ptr(), au.data_ptr(),
+                   ru.data_ptr(), False, tok.data_ptr(), nacc.data_ptr())
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(steps):
+        step()
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    n = nacc.cpu().numpy()
+    nbytes = int(sum(16 * (min(int(s) + 1, k)) + (16 * V if s < k else 8 * V) for s in n))
+    res = {"rows_per_s": B / (ms * 1e-3), "ms_per_step": ms, "batch": B, "k": k, "vocab": V,
+           "accepted_per_row": float(n.mean()), "compulsory_bytes_per_step": nbytes,
+           "hbm_gbps": nbytes / (ms * 1e-3) / 1e9}
+    ctx.close()
+    return res
+
+
 def load_traffic(workload: str):
     f = ROOT / "profiles" / f"traffic_{workload}.json"
     if f.exists():
@@ -180,6 +276,8 @@ def main() -> None:
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--cpu-baseline-child", action="store_true")
     ap.add_argument("--pmc-probe", action="store_true", help="short run for rocprofv3 counter passes")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the other workloads (zipf32k, zipf152k, char65, spec32k verify)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     args = ap.parse_args()
 
@@ -261,6 +359,15 @@ def main() -> None:
     rows_per_s = B / (ms * 1e-3)
     gbps = algo_bytes / (ms * 1e-3) / 1e9
     kernel_gbps = algo_bytes / (kernel_ms * 1e-3) / 1e9 if calls else None
+    others = None
+    if not args.no_other_configs:
+        others = {}
+        for name in ("char65", "zipf32k", "zipf152k"):
+            if name != args.workload:
+                print(f"[bench] other config {name}", file=sys.stderr, flush=True)
+                others[name] = bench_config(name)
+        print("[bench] other config spec32k (verify)", file=sys.stderr, flush=True)
+        others["spec32k"] = bench_verify()
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(args.workload, args.cpu_rows, args.cpu_reps)
     res = {
         "metric": METRIC,
@@ -285,6 +392,7 @@ def main() -> None:
                      "frac": kernel_gbps / PEAK_HBM_GBPS if kernel_gbps else None,
                      "traffic": load_traffic(args.workload), "kernel": "k_sample_chunks"},
         "cpu_baseline": cpu,
+        "other_configs": others,
     }
     print(json.dumps(res), flush=True)
     ctx.close()
