@@ -1,0 +1,112 @@
+"""The history-span form of plh_sample, plh_append_ids and plh_copy_rows
+(needs an MI355X): spans give the same ids as CSR offsets over the same
+histories (overlapping and empty spans included); the append skips negative
+positions; the strided copy places [B, V] blocks."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from pagellm_amd import _native
+from pagellm_amd.params import SamplingParams
+from pagellm_amd.sampling import _pack_params
+
+pytestmark = pytest.mark.gpu
+
+
+def _sample(c, x, params, u, hist_ids, hist_off, flags):
+    B, V = x.shape
+    t, k, p, r = _pack_params(params)
+    d = {n: c.to_device(a) for n, a in dict(x=x, t=t, k=k, p=p, r=r, u=u).items()}
+    hi = c.to_device(hist_ids)
+    ho = c.to_device(hist_off)
+    out = c.empty((B,), np.int32)
+    c.sample(d["x"].ptr, _native.dtype_code(x.dtype), V, B, V, hi.ptr, ho.ptr, d["t"].ptr, d["k"].ptr, d["p"].ptr,
+             d["r"].ptr, d["u"].ptr, out.ptr, None, flags)
+    return out.download()
+
+
+@pytest.mark.parametrize("rowwise", [False, True])
+def test_spans_match_csr(rowwise):
+    g = np.random.default_rng(3)
+    B, V = 12, 30000
+    x = g.normal(0, 2, (B, V)).astype(np.float32)
+    hists = [list(g.integers(0, V, g.integers(0, 400))) for _ in range(B)]
+    hists[3] = []
+    hists[5] = list(hists[4])  # same ids as row 4
+    params = [SamplingParams(temperature=[0.0, 1.0, 0.8][b % 3], top_k=[0, 40][b % 2], top_p=[1.0, 0.9][b % 2],
+                             repetition_penalty=1.3) for b in range(B)]
+    u = g.random(B)
+    off = np.zeros(B + 1, dtype=np.int64)
+    for b in range(B):
+        off[b + 1] = off[b] + len(hists[b])
+    ids = np.concatenate([np.asarray(h, dtype=np.int32) for h in hists])
+    # spans: rows 4 and 5 share one stored copy; the slab has gaps
+    slab, spans = [], np.zeros(2 * B, dtype=np.int64)
+    for b in range(B):
+        if b == 5:
+            spans[10], spans[11] = spans[8], spans[9]
+            continue
+        slab.extend([0] * 7)  # unused ids between histories
+        spans[2 * b] = len(slab)
+        slab.extend(hists[b])
+        spans[2 * b + 1] = len(slab)
+    slab = np.asarray(slab, dtype=np.int32)
+    c = _native.Context(0)
+    flags = _native.PLH_SAMPLE_ROWWISE if rowwise else 0
+    a = _sample(c, x, params, u, ids, off, flags)
+    s = _sample(c, x, params, u, slab, spans, flags | _native.PLH_SAMPLE_HIST_SPANS)
+    assert np.array_equal(a, s)
+    for b in range(B):
+        assert s[b] == oracle.sample(x[b], params[b], u[b], hists[b]), b
+    c.close()
+
+
+def test_append_ids_and_copy_rows():
+    c = _native.Context(0)
+    slab = c.to_device(np.full(16, -7, dtype=np.int32))
+    pos = c.to_device(np.array([3, -1, 0, 15], dtype=np.int64))
+    ids = c.to_device(np.array([30, 31, 32, 33], dtype=np.int32))
+    c.append_ids(slab.ptr, pos.ptr, ids.ptr, 4)
+    got = slab.download()
+    want = np.full(16, -7, dtype=np.int32)
+    want[[3, 0, 15]] = [30, 32, 33]
+    assert np.array_equal(got, want)
+    B, k, V = 3, 4, 5
+    src = np.arange(B * V, dtype=np.float64).reshape(B, V)
+    d_src = c.to_device(src)
+    dst = c.to_device(np.zeros((B, k, V)))
+    c.copy_rows(dst.ptr + 8 * 2 * V, 8 * k * V, d_src.ptr, 8 * V, 8 * V, B)
+    out = dst.download()
+    assert np.array_equal(out[:, 2], src)
+    assert not out[:, [0, 1, 3]].any()
+    c.close()
+
+
+def test_quantized_logits_general_path():
+    """bf16-like logits (8 mantissa bits): long runs of equal values at the
+    top-k and top-p cuts, through the row-wise general pipeline."""
+    g = np.random.default_rng(9)
+    B, V = 16, 50000
+    x = g.normal(0, 2, (B, V))
+    m, e = np.frexp(x)
+    x = np.ldexp(np.round(m * 256) / 256, e).astype(np.float32)
+    params = [SamplingParams(temperature=1.0, top_p=[0.5, 0.9, 0.99, 0.999][b % 4], top_k=[0, 0, 1000, 0][b % 4])
+              for b in range(B)]
+    u = g.random(B)
+    c = _native.Context(0)
+    t, k, p, r = _pack_params(params)
+    d = {n: c.to_device(a) for n, a in dict(x=x, t=t, k=k, p=p, r=r, u=u).items()}
+    out = c.empty((B,), np.int32)
+    c.sample(d["x"].ptr, _native.PLH_F32, V, B, V, None, None, d["t"].ptr, d["k"].ptr, d["p"].ptr, d["r"].ptr,
+             d["u"].ptr, out.ptr, None, _native.PLH_SAMPLE_ROWWISE)
+    ids = out.download()
+    from oracle.sampler import sample_boundary_gaps
+    for b in range(B):
+        ref = oracle.sample(x[b], params[b], u[b], ())
+        if ids[b] != ref:
+            gt, gd = sample_boundary_gaps(x[b], params[b], u[b], ())
+            assert gt < 1e-12 or gd < 1e-6, (b, int(ids[b]), ref)
+    c.close()
