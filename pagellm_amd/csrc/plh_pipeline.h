@@ -498,7 +498,7 @@ __device__ __forceinline__ int row_pipeline(Src& src, const RowParams& rp, int V
   const int n = src.n();
   constexpr int kG = Src::kGroup;
   constexpr int kPer = Src::kPer;
-  if (threadIdx.x < 64) sm.exp_tab[threadIdx.x] = exp2((double)threadIdx.x / 64.0);
+  if (threadIdx.x < 64) sm.exp_tab[threadIdx.x] = kExp2Frac64[threadIdx.x];
   __syncthreads();
 
   // ---- max / argmax of the penalised logits (sampling.py:73, :79, :106),
