@@ -356,8 +356,13 @@ int plh_verify(plh_ctx* c, const void* p, const void* q, int dtype, int B, int k
   int rc = use_device(c);
   if (rc != PLH_OK) return rc;
   plh::VerifyArgs a{p, q, B, k, V, draft, accept_u, draw_u, draw_u_per_stop ? 1 : 0, out_tokens, out_n_acc};
-  const hipError_t e = plh::launch_verify(a, dtype == PLH_F64, c->stream);
+  rc = reserve_ws(c, plh::verify_ws_bytes(B, V));
+  if (rc != PLH_OK) return rc;
+  const plh::VerifyWs ws = plh::verify_ws_layout(c->ws, B, V);
+  const hipError_t e = plh::launch_verify(a, ws, dtype == PLH_F64, c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "plh_verify launch");
+  PLH_HIP(c, hipEventRecord(c->ws_done, c->stream), "hipEventRecord");
+  c->ws_stream = c->stream;
   return PLH_OK;
 }
 

@@ -80,6 +80,13 @@ struct VerifyArgs {
   int32_t* out_n_acc;       // [B]
 };
 
+struct VerifyWs {
+  int32_t* stop;    // [B] stop position: first rejection, k, or -1
+  double* part;     // [B * C * 2] chunk sums of the residual and of p
+  uint64_t* fx;     // [B * C] chunk totals of the fixed-point weights
+  int C;            // chunks per row
+};
+
 hipError_t launch_sample_rows(const SampleArgs& a, bool f64, bool vec, hipStream_t s);
 // Fast path: workspace bytes for a [B, V] batch, its layout inside `base`
 // (256-byte aligned), and the two launches.
@@ -91,7 +98,11 @@ hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, int num_c
                               hipEvent_t between = nullptr);
 hipError_t launch_draw(const DrawArgs& a, bool f64, hipStream_t s);
 hipError_t launch_penalize(const PenalizeArgs& a, bool f64, hipStream_t s);
-hipError_t launch_verify(const VerifyArgs& a, bool f64, hipStream_t s);
+// Verify: workspace bytes for B rows of V tokens, its layout, and the three
+// launches (stop positions and chunk sums, chunk fixed-point totals, draw).
+size_t verify_ws_bytes(int B, int V);
+VerifyWs verify_ws_layout(void* base, int B, int V);
+hipError_t launch_verify(const VerifyArgs& a, const VerifyWs& ws, bool f64, hipStream_t s);
 hipError_t launch_append(int32_t* slab, const int64_t* pos, const int32_t* ids, int n, hipStream_t s);
 
 }  // namespace plh

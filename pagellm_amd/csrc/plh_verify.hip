@@ -1,5 +1,5 @@
-// gfx950 kernel for speculative decoding's accept/resample step
-// (src/pagellm/engine/speculative.py:38-60), one workgroup per sequence.
+// gfx950 kernels for speculative decoding's accept/resample step
+// (src/pagellm/engine/speculative.py:38-60).
 //
 // The k accept tests are k gathered scalars: accept x_i while
 // u_i < min(1, p_i[x_i] / q_i[x_i]) (strict), stop at the first rejection.
@@ -7,40 +7,183 @@
 // residual max(p_i - q_i, 0) (or p_i when the residual is all zero), after k
 // acceptances the bonus row p_k; the emitted token is an inverse-CDF draw
 // over that row.
+//
+// A row's draw is spread over chunks of 4096 tokens, one workgroup each, so
+// that a batch of a few dozen rows still fills the chip:
+//   k_verify_parts  (row, chunk)  stop position; float64 chunk sums of the
+//                                 residual and of p;
+//   k_verify_fx     (row, chunk)  the row's total W from the chunk sums (one
+//                                 fixed order, the same in every workgroup);
+//                                 the chunk's total of the fixed-point
+//                                 weights round(w / W * 2^62);
+//   k_verify_draw   (row)         t = floor(u * sum of chunk totals); the
+//                                 chunk whose exact running total first
+//                                 exceeds t, rescanned for the token.
+// The fixed-point sums are exact integers, so the chunk found by the
+// running totals always holds the crossing token, whatever the order of
+// the additions.
 #include "plh_kernels.h"
 #include "plh_pipeline.h"
 
 namespace plh {
 
+constexpr int kVPer = 8;                   // tokens per thread in a chunk
+constexpr int kVChunk = kVPer * kThreads;  // tokens per chunk
+
+__host__ __device__ constexpr int verify_chunks(int V) { return (V + kVChunk - 1) / kVChunk; }
+
+// Stop position of row b (speculative.py:51-60): the first i < k whose
+// draft id is out of range (-1) or whose accept test fails (i), else k.
+// Computed by each calling wave on its own (k gathers per 64 tests).
 template <typename TIn>
-__global__ __launch_bounds__(kThreads) void k_verify(VerifyArgs a) {
-  __shared__ double redd[kWaves];
-  __shared__ uint64_t redu[kWaves];
-  __shared__ int redi[kWaves];
-  __shared__ int s_stop;
-  const int b = blockIdx.x;
+__device__ __forceinline__ int stop_position(const VerifyArgs& a, const TIn* P, const TIn* Q, int b) {
+  const int k = a.k, V = a.V;
+  for (int base = 0; base < k; base += kWave) {
+    const int i = base + lane();
+    bool bad = false, stop = false;
+    if (i < k) {
+      const int x = a.draft[(size_t)b * k + i];
+      bad = x < 0 || x >= V;  // rejected by the host wrapper; never index with it
+      if (!bad) {
+        const double r = (double)P[(size_t)i * V + x] / (double)Q[(size_t)i * V + x];
+        const double thr = r < 1.0 ? r : 1.0;  // Python min(1.0, r): NaN -> 1.0
+        stop = !(a.accept_u[(size_t)b * k + i] < thr);
+      }
+    }
+    const uint64_t m = __ballot(bad || stop);
+    if (m != 0) {
+      const int f = __builtin_ctzll(m);
+      return lane_value((int)bad, f) ? -1 : base + f;
+    }
+  }
+  return k;
+}
+
+// What the draw reads from row b's stop position s: the residual
+// max(p_s - q_s, 0) unless it sums to zero (speculative.py:55-58), else
+// max(p_s, 0); and its float64 total W.  W comes from the chunk sums in one
+// fixed order (lane j adds chunks j, j + 64, ..., then the wave's sum tree),
+// so every wave of every launch gets the same bits.
+struct DrawTotal {
+  bool resid;
+  double W;
+};
+
+__device__ __forceinline__ DrawTotal draw_total(const VerifyWs& ws, int b, int s, int k) {
+  const int C = ws.C;
+  const double* part = ws.part + (size_t)b * C * 2;
+  double sr = 0.0, sp = 0.0;
+  for (int j = lane(); j < C; j += kWave) {
+    sr += part[2 * j];
+    sp += part[2 * j + 1];
+  }
+  sr = wave_sum(sr);
+  sp = wave_sum(sp);
+  const bool resid = s < k && sr > 0.0;
+  return DrawTotal{resid, resid ? sr : sp};
+}
+
+// The draw weight of one token from its p and q values (q is ignored unless
+// the draw is over the residual); tokens past V weigh nothing.
+__device__ __forceinline__ double draw_weight(double p, double q, bool resid, bool in_row) {
+  const double v = p - (resid ? q : 0.0);
+  return in_row && v > 0.0 ? v : 0.0;
+}
+
+template <typename TIn>
+__global__ __launch_bounds__(kThreads) void k_verify_parts(VerifyArgs a, VerifyWs ws) {
+  __shared__ double red[2][kWaves];
+  const int C = ws.C;
+  const int b = blockIdx.x / C, c = blockIdx.x - b * C;
   const int k = a.k, V = a.V;
   const TIn* P = reinterpret_cast<const TIn*>(a.p) + (size_t)b * (k + 1) * V;
   const TIn* Q = reinterpret_cast<const TIn*>(a.q) + (size_t)b * k * V;
-  if (threadIdx.x == 0) {
-    int s = k;
-    for (int i = 0; i < k; ++i) {
-      const int x = a.draft[(size_t)b * k + i];
-      if (x < 0 || x >= V) {  // rejected by the host wrapper; never index with it
-        s = -1;
-        break;
-      }
-      const double r = (double)P[(size_t)i * V + x] / (double)Q[(size_t)i * V + x];
-      const double thr = r < 1.0 ? r : 1.0;  // Python min(1.0, r): NaN -> 1.0
-      if (!(a.accept_u[(size_t)b * k + i] < thr)) {
-        s = i;
-        break;
-      }
+  const int s = stop_position(a, P, Q, b);
+  if (c == 0 && threadIdx.x == 0) ws.stop[b] = s;
+  if (s < 0) return;
+  const TIn* ps = P + (size_t)s * V;
+  const int i0 = c * kVChunk + (int)threadIdx.x;
+  double sr = 0.0, sp = 0.0;
+  if (s < k) {
+    const TIn* qs = Q + (size_t)s * V;
+    TIn pv[kVPer], qv[kVPer];
+#pragma unroll
+    for (int l = 0; l < kVPer; ++l) {
+      const int i = i0 + l * kThreads;
+      pv[l] = i < V ? ps[i] : TIn(0);
+      qv[l] = i < V ? qs[i] : TIn(0);
     }
-    s_stop = s;
+#pragma unroll
+    for (int l = 0; l < kVPer; ++l) {
+      const double d = (double)pv[l] - (double)qv[l];
+      sr += d > 0.0 ? d : 0.0;
+      sp += (double)pv[l] > 0.0 ? (double)pv[l] : 0.0;
+    }
+  } else {
+    TIn pv[kVPer];
+#pragma unroll
+    for (int l = 0; l < kVPer; ++l) {
+      const int i = i0 + l * kThreads;
+      pv[l] = i < V ? ps[i] : TIn(0);
+    }
+#pragma unroll
+    for (int l = 0; l < kVPer; ++l) sp += (double)pv[l] > 0.0 ? (double)pv[l] : 0.0;
   }
-  __syncthreads();
-  const int s = s_stop;
+  sr = wave_sum(sr);
+  sp = wave_sum(sp);
+  if (lane() == 0) {
+    red[0][wave()] = sr;
+    red[1][wave()] = sp;
+  }
+  wg_barrier();
+  if (threadIdx.x == 0) {
+    double tr = red[0][0], tp = red[1][0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+      tr += red[0][w];
+      tp += red[1][w];
+    }
+    ws.part[2 * (size_t)blockIdx.x] = tr;
+    ws.part[2 * (size_t)blockIdx.x + 1] = tp;
+  }
+}
+
+template <typename TIn>
+__global__ __launch_bounds__(kThreads) void k_verify_fx(VerifyArgs a, VerifyWs ws) {
+  __shared__ uint64_t redu[kWaves];
+  const int C = ws.C;
+  const int b = blockIdx.x / C, c = blockIdx.x - b * C;
+  const int k = a.k, V = a.V;
+  const int s = ws.stop[b];
+  if (s < 0) return;
+  const TIn* ps = reinterpret_cast<const TIn*>(a.p) + ((size_t)b * (k + 1) + s) * V;
+  const TIn* qs = s < k ? reinterpret_cast<const TIn*>(a.q) + ((size_t)b * k + s) * V : ps;
+  // loads first, all in flight together (indices clamped into the row)
+  const int i0 = c * kVChunk + (int)threadIdx.x;
+  TIn pv[kVPer], qv[kVPer];
+#pragma unroll
+  for (int l = 0; l < kVPer; ++l) {
+    const int i = min(i0 + l * kThreads, V - 1);
+    pv[l] = ps[i];
+    qv[l] = qs[i];
+  }
+  const DrawTotal d = draw_total(ws, b, s, k);
+  if (!(d.W > 0.0)) return;  // the draw takes V - 1 without reading the totals
+  uint64_t t = 0;
+#pragma unroll
+  for (int l = 0; l < kVPer; ++l)
+    t += to_fx(draw_weight((double)pv[l], (double)qv[l], d.resid, i0 + l * kThreads < V) / d.W);
+  t = block_sum<uint64_t>(t, redu);
+  if (threadIdx.x == 0) ws.fx[blockIdx.x] = t;
+}
+
+template <typename TIn>
+__global__ __launch_bounds__(kThreads) void k_verify_draw(VerifyArgs a, VerifyWs ws) {
+  __shared__ uint64_t redu[kWaves];
+  __shared__ int redi[kWaves];
+  const int b = blockIdx.x;
+  const int k = a.k, V = a.V, C = ws.C;
+  const int s = ws.stop[b];
   int32_t* out = a.out_tokens + (size_t)b * (k + 1);
   if (s < 0) {
     for (int i = threadIdx.x; i <= k; i += kThreads) out[i] = -1;
@@ -48,33 +191,59 @@ __global__ __launch_bounds__(kThreads) void k_verify(VerifyArgs a) {
     return;
   }
   const double u = a.draw_u_per_stop ? a.draw_u[(size_t)b * (k + 1) + s] : a.draw_u[b];
-  int tok;
-  if (s < k) {
-    const TIn* ps = P + (size_t)s * V;
-    const TIn* qs = Q + (size_t)s * V;
-    auto resid = [&](int i) -> double {
-      const double d = (double)ps[i] - (double)qs[i];
-      return d > 0.0 ? d : 0.0;
-    };
-    double sr = 0.0;
-    for (int i = threadIdx.x; i < V; i += kThreads) sr += resid(i);
-    sr = block_sum(sr, redd);
-    if (sr > 0.0) {
-      tok = draw_weights(resid, V, u, redd, redu, redi);
-    } else {
-      auto pw = [&](int i) -> double {
-        const double v = (double)ps[i];
-        return v > 0.0 ? v : 0.0;
-      };
-      tok = draw_weights(pw, V, u, redd, redu, redi);
+  const DrawTotal d = draw_total(ws, b, s, k);
+  int tok = V - 1;  // sampling.py:98: no crossing (or no mass) takes the last id
+  if (d.W > 0.0) {
+    const uint64_t* fx = ws.fx + (size_t)b * C;
+    uint64_t tf = 0;
+    for (int j = lane(); j < C; j += kWave) tf += fx[j];
+    tf = wave_sum(tf);
+    const uint64_t t_fx = (uint64_t)__double2ull_rd(u * (double)tf);
+    // the first chunk whose running total exceeds t_fx (every wave alike)
+    int cs = -1;
+    uint64_t before = 0, run = 0;
+    for (int base = 0; base < C && cs < 0; base += kWave) {
+      const int j = base + lane();
+      const uint64_t v = j < C ? fx[j] : 0ull;
+      const uint64_t incl = run + wave_scan_incl(v, (uint64_t)0, OpAdd{});
+      const uint64_t m = __ballot(j < C && incl > t_fx);
+      if (m != 0) {
+        const int f = __builtin_ctzll(m);
+        cs = base + f;
+        before = lane_value(incl - v, f);
+      }
+      run = lane_value(incl, kWave - 1);
     }
-  } else {
-    const TIn* pk = P + (size_t)k * V;
-    auto pw = [&](int i) -> double {
-      const double v = (double)pk[i];
-      return v > 0.0 ? v : 0.0;
-    };
-    tok = draw_weights(pw, V, u, redd, redu, redi);
+    if (cs >= 0) {
+      // rescan that chunk in thread order: the same weights, the same exact total
+      const uint64_t tgt = t_fx - before;
+      const TIn* ps = reinterpret_cast<const TIn*>(a.p) + ((size_t)b * (k + 1) + s) * V;
+      const TIn* qs = s < k ? reinterpret_cast<const TIn*>(a.q) + ((size_t)b * k + s) * V : ps;
+      const int i0 = cs * kVChunk + (int)threadIdx.x * kVPer;
+      TIn pv[kVPer], qv[kVPer];
+#pragma unroll
+      for (int l = 0; l < kVPer; ++l) {
+        const int i = min(i0 + l, V - 1);
+        pv[l] = ps[i];
+        qv[l] = qs[i];
+      }
+      uint64_t w[kVPer], ts = 0;
+#pragma unroll
+      for (int l = 0; l < kVPer; ++l) {
+        w[l] = to_fx(draw_weight((double)pv[l], (double)qv[l], d.resid, i0 + l < V) / d.W);
+        ts += w[l];
+      }
+      uint64_t tt;
+      uint64_t cum = block_excl_scan<uint64_t>(ts, redu, &tt);
+      int my = INT_MAX;
+#pragma unroll
+      for (int l = 0; l < kVPer; ++l) {
+        cum += w[l];
+        if (my == INT_MAX && cum > tgt) my = i0 + l;
+      }
+      const int f = block_min<int>(my, redi);
+      if (f != INT_MAX) tok = f;
+    }
   }
   if (threadIdx.x == 0) {
     const int32_t* dr = a.draft + (size_t)b * k;
@@ -85,10 +254,40 @@ __global__ __launch_bounds__(kThreads) void k_verify(VerifyArgs a) {
   }
 }
 
-hipError_t launch_verify(const VerifyArgs& a, bool f64, hipStream_t s) {
-  if (f64) hipLaunchKernelGGL((k_verify<double>), dim3(a.B), dim3(kThreads), 0, s, a);
-  else hipLaunchKernelGGL((k_verify<float>), dim3(a.B), dim3(kThreads), 0, s, a);
+namespace {
+size_t up256(size_t v) { return (v + 255) / 256 * 256; }
+}  // namespace
+
+size_t verify_ws_bytes(int B, int V) {
+  const size_t n = (size_t)B * verify_chunks(V);
+  return up256((size_t)B * sizeof(int32_t)) + up256(n * 2 * sizeof(double)) + up256(n * sizeof(uint64_t));
+}
+
+VerifyWs verify_ws_layout(void* base, int B, int V) {
+  VerifyWs w{};
+  w.C = verify_chunks(V);
+  const size_t n = (size_t)B * w.C;
+  char* p = static_cast<char*>(base);
+  w.stop = reinterpret_cast<int32_t*>(p);
+  p += up256((size_t)B * sizeof(int32_t));
+  w.part = reinterpret_cast<double*>(p);
+  p += up256(n * 2 * sizeof(double));
+  w.fx = reinterpret_cast<uint64_t*>(p);
+  return w;
+}
+
+template <typename TIn>
+hipError_t launch_verify_t(const VerifyArgs& a, const VerifyWs& ws, hipStream_t s) {
+  const dim3 block(kThreads);
+  const dim3 grid_parts((unsigned)((size_t)a.B * ws.C));
+  hipLaunchKernelGGL((k_verify_parts<TIn>), grid_parts, block, 0, s, a, ws);
+  hipLaunchKernelGGL((k_verify_fx<TIn>), grid_parts, block, 0, s, a, ws);
+  hipLaunchKernelGGL((k_verify_draw<TIn>), dim3(a.B), block, 0, s, a, ws);
   return hipGetLastError();
+}
+
+hipError_t launch_verify(const VerifyArgs& a, const VerifyWs& ws, bool f64, hipStream_t s) {
+  return f64 ? launch_verify_t<double>(a, ws, s) : launch_verify_t<float>(a, ws, s);
 }
 
 }  // namespace plh

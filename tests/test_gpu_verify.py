@@ -106,3 +106,40 @@ def test_verify_edge_cases():
     assert n[0] == 0
     with pytest.raises(IndexError):
         verify_batch(p[None], q[None], [[0, 2]], [[0.1, 0.1]], [0.5])
+
+
+def test_verify_draw_across_chunks():
+    """Rows longer than one 4096-token chunk, with the draw's mass placed in
+    chosen chunks (the rest zero), a ragged last chunk, uniforms swept to
+    both ends, and more draft tokens than one wave tests at once."""
+    g = np.random.default_rng(21)
+    V = 3 * 4096 + 17
+    rows_p, rows_q, drafts, aus, dus = [], [], [], [], []
+    k = 70
+    for b in range(12):
+        p = np.zeros((k + 1, V))
+        q = np.zeros((k, V))
+        for i in range(k + 1):
+            # mass in one chunk, two chunks, or spread, by row
+            lo, hi = [(0, V), (4096, 8192), (3 * 4096, V), (4095, 4097)][b % 4]
+            p[i, lo:hi] = _dist(g, hi - lo, 2.0)
+        for i in range(k):
+            q[i] = p[i]
+            # a rejection at b % k: q moves mass off the draft token's chunk
+            if i == b % 5:
+                q[i] = _dist(g, V, 0.5)
+        draft = [int(np.argmax(q[i])) for i in range(k)]
+        rows_p.append(p)
+        rows_q.append(q)
+        drafts.append(draft)
+        aus.append(np.full(k, 0.5) if b % 3 else np.full(k, 1e-300))
+        dus.append([0.0, 0.999999999, 0.5, 0.25][b % 4])
+    P, Q = np.stack(rows_p), np.stack(rows_q)
+    for dt in (np.float64, np.float32):
+        toks, n = verify_batch(P.astype(dt), Q.astype(dt), drafts, np.stack(aus), dus)
+        Pc, Qc = P.astype(dt).astype(np.float64), Q.astype(dt).astype(np.float64)
+        rt, rn = oracle.verify_batch(Pc, Qc, np.array(drafts), np.stack(aus), np.array(dus))
+        for b in range(len(n)):
+            if n[b] != rn[b] or not np.array_equal(toks[b], rt[b]):
+                gap = verify_boundary_gap(Pc[b], Qc[b], drafts[b], aus[b], dus[b])
+                assert gap < 1e-6, (dt, b, n[b], rn[b], gap)
