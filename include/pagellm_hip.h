@@ -167,6 +167,23 @@ int plh_copy_rows(plh_ctx* ctx, void* dst, int64_t dst_pitch, const void* src, i
  */
 int plh_append_ids(plh_ctx* ctx, int32_t* slab, const int64_t* pos, const int32_t* ids, int n);
 
+/*
+ * The logits producer: the model's final RMSNorm and lm_head product,
+ * replacing src/pagellm/model/transformer.py:271
+ * (rms_norm(h, self.w["norm"], eps) @ self.w["lm_head"], rms_norm at :79-82)
+ * for float32 models, written into a logits buffer plh_sample can read in
+ * place:
+ *   r_n = 1 / sqrt(mean_d(h[n, d]^2) + eps)      (float32, eps as a float32)
+ *   out[n, v] = sum_d ((h[n, d] * r_n) * norm[d]) * W[d, v]
+ * for n < N, v < V, with the products and sums in float32 on the matrix
+ * cores.  h [N, ldh], norm [D], W [D, ldw] (row-major: the reference's
+ * [D, V] lm_head) and out [N, ldo] are float32 device pointers; the
+ * normalised rows live in the context's workspace.  Ordered on the
+ * context's stream.
+ */
+int plh_rmsnorm_lm_head(plh_ctx* ctx, const float* h, int64_t ldh, int N, int D, const float* norm, double eps,
+                        const float* W, int64_t ldw, int V, float* out, int64_t ldo);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,4 +1,4 @@
-"""CPU oracle for the pagellm sampler: test infrastructure only.
+"""CPU oracle for the pagellm sampler and logits producer: test infrastructure only.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import this package, and only as the checker or as the timed
@@ -18,3 +18,4 @@ from .sampler import (  # noqa: F401
     verify_batch,
     verify_boundary_gap,
 )
+from .head import head_error_bound, lm_head_logits, rms_norm  # noqa: F401,E402

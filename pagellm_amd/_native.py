@@ -58,6 +58,10 @@ SIGNATURES = {
     ),
     "plh_append_ids": (_c_int, [_vp, _vp, _vp, _vp, _c_int]),
     "plh_copy_rows": (_c_int, [_vp, _vp, _c_i64, _vp, _c_i64, _c_i64, _c_int]),
+    "plh_rmsnorm_lm_head": (
+        _c_int,
+        [_vp, _vp, _c_i64, _c_int, _c_int, _vp, ctypes.c_double, _vp, _c_i64, _c_int, _vp, _c_i64],
+    ),
 }
 
 _lib = None
@@ -74,6 +78,16 @@ def load_library() -> ctypes.CDLL:
                     f"{LIB_PATH.name} is not built; run `python -m pagellm_amd.build` "
                     "(the sampler has no CPU fallback)"
                 )
+            # One HIP runtime per process.  torch's ROCm wheel bundles its own
+            # libamdhip64 (same soname as the system one); loaded first, it
+            # also serves this library, so torch tensors and streams and this
+            # library's calls share one runtime.  Loaded after the system
+            # runtime, it would bring a second HIP/HSA runtime into the
+            # process and torch would find no GPU.
+            try:
+                import torch  # noqa: F401
+            except ImportError:
+                pass
             lib = ctypes.CDLL(str(LIB_PATH))
             for name, (res, args) in SIGNATURES.items():
                 fn = getattr(lib, name)
@@ -247,6 +261,10 @@ class Context:
     def copy_rows(self, dst_ptr, dst_pitch, src_ptr, src_pitch, row_bytes, rows) -> None:
         self._check(self.lib.plh_copy_rows(self.handle, dst_ptr, int(dst_pitch), src_ptr, int(src_pitch),
                                            int(row_bytes), int(rows)))
+
+    def rmsnorm_lm_head(self, h_ptr, ldh, N, D, norm_ptr, eps, w_ptr, ldw, V, out_ptr, ldo) -> None:
+        self._check(self.lib.plh_rmsnorm_lm_head(self.handle, h_ptr, ldh, N, D, norm_ptr, eps, w_ptr, ldw, V,
+                                                 out_ptr, ldo))
 
     def append_ids(self, slab_ptr, pos_ptr, ids_ptr, n) -> None:
         self._check(self.lib.plh_append_ids(self.handle, slab_ptr, pos_ptr, ids_ptr, int(n)))

@@ -8,6 +8,8 @@
 #include <string>
 #include <vector>
 
+#include <cmath>
+
 #include "pagellm_hip.h"
 #include "plh_kernels.h"
 
@@ -390,6 +392,39 @@ int plh_append_ids(plh_ctx* c, int32_t* slab, const int64_t* pos, const int32_t*
   if (rc != PLH_OK) return rc;
   const hipError_t e = plh::launch_append(slab, pos, ids, n, c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "plh_append_ids launch");
+  return PLH_OK;
+}
+
+int plh_rmsnorm_lm_head(plh_ctx* c, const float* h, int64_t ldh, int N, int D, const float* norm, double eps,
+                        const float* W, int64_t ldw, int V, float* out, int64_t ldo) {
+  if (c == nullptr) return PLH_ERR_INVALID_ARG;
+  if (N < 0 || D < 1 || V < 1) return fail(c, PLH_ERR_INVALID_ARG, "need N >= 0, D >= 1 and V >= 1%s");
+  if (N == 0) return PLH_OK;
+  if (ldh < D || ldw < V || ldo < V) return fail(c, PLH_ERR_INVALID_ARG, "need ldh >= D, ldw >= V and ldo >= V%s");
+  if (h == nullptr || norm == nullptr || W == nullptr || out == nullptr)
+    return fail(c, PLH_ERR_INVALID_ARG, "null device pointer%s");
+  if (!(eps >= 0.0) || !std::isfinite(eps)) return fail(c, PLH_ERR_INVALID_ARG, "eps must be finite and >= 0%s");
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  rc = reserve_ws(c, plh::head_ws_bytes(N, D));
+  if (rc != PLH_OK) return rc;
+  plh::HeadArgs a{};
+  a.h = h;
+  a.ldh = ldh;
+  a.norm = norm;
+  a.eps = (float)eps;
+  a.w = W;
+  a.ldw = ldw;
+  a.out = out;
+  a.ldo = ldo;
+  a.act = static_cast<float*>(c->ws);
+  a.N = N;
+  a.D = D;
+  a.V = V;
+  const hipError_t e = plh::launch_head(a, c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "plh_rmsnorm_lm_head launch");
+  PLH_HIP(c, hipEventRecord(c->ws_done, c->stream), "hipEventRecord");
+  c->ws_stream = c->stream;
   return PLH_OK;
 }
 

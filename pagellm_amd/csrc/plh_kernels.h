@@ -87,6 +87,20 @@ struct VerifyWs {
   int C;            // chunks per row
 };
 
+struct HeadArgs {
+  const float* h;     // [N, ldh] final hidden states
+  int64_t ldh;
+  const float* norm;  // [D] RMSNorm weight
+  float eps;
+  const float* w;     // [D, ldw] lm_head, the reference's [D, V] layout
+  int64_t ldw;
+  float* out;         // [N, ldo] logits
+  int64_t ldo;
+  float* act;         // workspace [N, lda]: normalised rows, zero-padded
+  int64_t lda;
+  int N, D, V;
+};
+
 hipError_t launch_sample_rows(const SampleArgs& a, bool f64, bool vec, hipStream_t s);
 // Fast path: workspace bytes for a [B, V] batch, its layout inside `base`
 // (256-byte aligned), and the two launches.
@@ -103,6 +117,10 @@ hipError_t launch_penalize(const PenalizeArgs& a, bool f64, hipStream_t s);
 size_t verify_ws_bytes(int B, int V);
 VerifyWs verify_ws_layout(void* base, int B, int V);
 hipError_t launch_verify(const VerifyArgs& a, const VerifyWs& ws, bool f64, hipStream_t s);
+// Logits producer: workspace bytes (the normalised rows) and the two
+// launches (RMSNorm, then the MFMA product into out).
+size_t head_ws_bytes(int N, int D);
+hipError_t launch_head(HeadArgs a, hipStream_t s);
 hipError_t launch_append(int32_t* slab, const int64_t* pos, const int32_t* ids, int n, hipStream_t s);
 
 }  // namespace plh

@@ -75,6 +75,7 @@ def test_null_context_is_an_invalid_argument(lib):
     assert lib.plh_kernel_times(None, None, None, None) == -1
     assert lib.plh_append_ids(None, None, None, None, 1) == -1
     assert lib.plh_copy_rows(None, None, 8, None, 8, 8, 1) == -1
+    assert lib.plh_rmsnorm_lm_head(None, None, 4, 1, 4, None, 1e-5, None, 4, 4, None, 4) == -1
     assert lib.plh_last_error(None) == b"null context"
     lib.plh_destroy(None)
 
