@@ -40,6 +40,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBPS = 8000.0
+PEAK_FP32_MFMA_TFLOPS = 157.3
 METRIC = "sampled rows/sec + HBM GB/s (% peak), batch 256 × vocab 128256 fp32"
 
 
@@ -254,6 +255,50 @@ def bench_verify(steps: int = 50, warmup: int = 5) -> dict:
     return res
 
 
+def bench_head(steps: int = 20, warmup: int = 3, N: int = 256, D: int = 4096, V: int = 128256) -> dict:
+    """The logits producer at the sampler's headline shape: final RMSNorm and
+    lm_head (256 rows, model width 4096, 128 256-token vocabulary, float32
+    weights resident in HBM, random-init) writing the logits the sampler
+    reads.  Reports launches/s of the pair and the product's float32 matrix
+    rate against the 157.3 TFLOP/s fp32 MFMA peak."""
+    import torch
+
+    from pagellm_amd import _native
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    h = torch.randn((N, D), device=dev, dtype=torch.float32, generator=g)
+    norm = 1 + 0.1 * torch.randn(D, device=dev, dtype=torch.float32, generator=g)
+    W = 0.02 * torch.randn((D, V), device=dev, dtype=torch.float32, generator=g)
+    out = torch.empty((N, V), device=dev, dtype=torch.float32)
+    stream = torch.cuda.Stream(device=dev)
+    ctx = _native.Context(0)
+    ctx.set_stream(stream.cuda_stream)
+    torch.cuda.synchronize()
+
+    def step():
+        ctx.rmsnorm_lm_head(h.data_ptr(), D, N, D, norm.data_ptr(), 1e-5, W.data_ptr(), V, V, out.data_ptr(), V)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(steps):
+        step()
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    flops = 2.0 * N * D * V
+    tflops = flops / (ms * 1e-3) / 1e12
+    res = {"launches_per_s": 1e3 / ms, "ms_per_step": ms, "rows": N, "width": D, "vocab": V,
+           "dtype": "fp32", "flop_per_step": flops, "tflops": tflops, "mfma_fp32_frac": tflops / PEAK_FP32_MFMA_TFLOPS,
+           "weight_bytes": 4 * D * V, "weight_gbps": 4.0 * D * V / (ms * 1e-3) / 1e9}
+    ctx.close()
+    return res
+
+
 def load_traffic(workload: str):
     f = ROOT / "profiles" / f"traffic_{workload}.json"
     if f.exists():
@@ -368,6 +413,8 @@ def main() -> None:
                 others[name] = bench_config(name)
         print("[bench] other config spec32k (verify)", file=sys.stderr, flush=True)
         others["spec32k"] = bench_verify()
+        print("[bench] other config head128k (logits producer)", file=sys.stderr, flush=True)
+        others["head128k"] = bench_head()
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(args.workload, args.cpu_rows, args.cpu_reps)
     res = {
         "metric": METRIC,

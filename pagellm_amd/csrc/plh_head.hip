@@ -3,18 +3,22 @@
 // (src/pagellm/model/transformer.py:79-82, :271), in float32 as the
 // reference computes it, written straight into the sampler's logits buffer.
 //
-//   k_head_rmsnorm  one workgroup per row: r = 1 / sqrt(mean(h * h) + eps)
+//   k_head_rms      one workgroup per row: r = 1 / sqrt(mean(h * h) + eps)
 //                   in float32 (the squares summed in float64 and rounded
-//                   once), act = (h * r) * norm, zero-padded to a multiple of
-//                   32 columns;
+//                   once);
+//   k_head_act      act = (h * r) * norm, stored k-major and zero-padded to
+//                   whole tiles (32 in k, 256 in n);
 //   k_head_gemm     out = act @ W on the fp32 matrix cores
 //                   (v_mfma_f32_32x32x2_f32, products and sums in float32).
-//                   A workgroup of 8 waves owns a 256-row x 256-column tile
-//                   of out; each wave a 64 x 128 block, 2 x 4 MFMA tiles
-//                   held in 128 accumulator registers.  The k dimension
-//                   streams through LDS 32 at a time, double-buffered: the
-//                   next stage's global loads are in flight while the
-//                   matrix cores work on the current one.
+//                   A workgroup of 8 waves (two per SIMD) owns a 256-row x
+//                   256-column tile of out; each wave a 64 x 128 block,
+//                   2 x 4 MFMA tiles held in 128 accumulator registers.
+//                   Both operands are k-major in LDS (each half-wave reads
+//                   32 consecutive floats per MFMA operand); k streams
+//                   through LDS 32 at a time, double-buffered: the next
+//                   stage's global loads are in flight, and its LDS stores
+//                   trickle in, while the matrix cores work on the current
+//                   one.
 #include "plh_device.h"
 #include "plh_kernels.h"
 
@@ -22,17 +26,17 @@ namespace plh {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kHeadRows = 256;             // rows of out per workgroup
 constexpr int kHeadCols = 256;             // vocabulary columns per workgroup
 constexpr int kHeadK = 32;                 // k per LDS stage
-constexpr int kAStride = kHeadK + 2;       // act tile row pitch (floats)
-constexpr int kBStride = kHeadCols + 32;   // W tile row pitch (floats)
+constexpr int kTileStride = 256 + 32;      // LDS row pitch of both tiles (floats)
 
 __host__ __device__ constexpr int head_kpad(int D) { return (D + kHeadK - 1) / kHeadK * kHeadK; }
+__host__ __device__ constexpr int head_npad(int N) { return (N + kHeadRows - 1) / kHeadRows * kHeadRows; }
 
-__global__ __launch_bounds__(kThreads) void k_head_rmsnorm(HeadArgs a) {
+// r_n = 1 / sqrt(mean(h[n] * h[n]) + eps), one workgroup per row.
+__global__ __launch_bounds__(kThreads) void k_head_rms(HeadArgs a) {
   __shared__ double red[kWaves];
   const int n = blockIdx.x;
   const float* x = a.h + (size_t)n * a.ldh;
@@ -44,70 +48,120 @@ __global__ __launch_bounds__(kThreads) void k_head_rmsnorm(HeadArgs a) {
   s = block_sum(s, red);
   // np.mean in float32, + eps as a float32 (a Python float is a weak
   // scalar), float32 sqrt and reciprocal (transformer.py:81)
-  const float mean = (float)s / (float)a.D;
-  const float r = 1.0f / sqrtf(mean + a.eps);
-  float* out = a.act + (size_t)n * a.lda;
-  const int Dp = head_kpad(a.D);
-  for (int d = threadIdx.x; d < Dp; d += kThreads) out[d] = d < a.D ? (x[d] * r) * a.norm[d] : 0.0f;  // :82
+  if (threadIdx.x == 0) {
+    const float mean = (float)s / (float)a.D;
+    a.rinv[n] = 1.0f / sqrtf(mean + a.eps);
+  }
 }
 
-struct HeadSmem {
-  float a[2][kHeadRows * kAStride];
-  float b[2][kHeadK * kBStride];
+// act[d][n] = (h[n][d] * r_n) * norm[d] (transformer.py:82), stored k-major
+// ([Dp][lda], lda = N rounded up to the row tile) and zero outside
+// d < D, n < N: a 32 (d) x 64 (n) block per workgroup, transposed through LDS
+// so that both the reads of h and the writes of act are 16-byte and
+// contiguous.
+__global__ __launch_bounds__(kThreads) void k_head_act(HeadArgs a) {
+  __shared__ float t[64][32 + 1];
+  const int d0 = blockIdx.x * 32, n0 = blockIdx.y * 64;
+  const int tid = threadIdx.x;
+  {
+    const int nl = tid >> 3, dl = (tid & 7) * 4;  // 64 rows x 8 groups of 4
+    const int n = n0 + nl;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (n < a.N) {
+      const float r = a.rinv[n];
+      const float* x = a.h + (size_t)n * a.ldh;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = d0 + dl + e;
+        if (d < a.D) v[e] = (x[d] * r) * a.norm[d];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t[nl][dl + e] = v[e];
+  }
+  wg_barrier();
+  {
+    const int dl = tid >> 4, nl = (tid & 15) * 4;  // 32 rows x 16 groups of 4
+    f32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = t[nl + e][dl];
+    *reinterpret_cast<f32x4*>(a.act + (size_t)(d0 + dl) * a.lda + n0 + nl) = v;
+  }
+}
+
+// 16-byte aligned, so that the stage stores are single ds_write_b128s
+struct __attribute__((aligned(16))) HeadSmem {
+  float a[2][kHeadK * kTileStride];  // act stage, [k][n]
+  float b[2][kHeadK * kTileStride];  // W stage, [k][v]
 };
 
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_head_gemm(HeadArgs a) {
-  __shared__ HeadSmem sm;
+// Wave layout: each wave owns kMT x 4 MFMA tiles (kMT * 32 rows x 128
+// columns) of the workgroup's 256 x 256 tile.  kMT = 2: 8 waves, two per
+// SIMD, 128 accumulators each; kMT = 4: 4 waves, one per SIMD, 256.
+constexpr int kMT = 2;
+constexpr int kWavesN = kHeadRows / (32 * kMT);
+constexpr int kGemmWaves = kWavesN * 2;
+constexpr int kGemmThreads = 64 * kGemmWaves;
+constexpr int kStageRows = kGemmThreads / 64;   // stage rows one pass of the workgroup moves
+constexpr int kStagePasses = kHeadK / kStageRows;
+// The next stage goes to LDS one pass (two ds_write_b128) per k step,
+// after steps kStoreStep .. kStoreStep + kStagePasses - 1, so that LDS
+// writes never arrive as a burst in front of the operand reads.
+constexpr int kStoreStep = 1;
+constexpr int kAhead = 1;                        // k steps the operand reads run ahead
+static_assert(kStoreStep + kStagePasses <= kHeadK / 2, "stage stores must end inside the k loop");
+
+// One workgroup tile.  VEC: every W row segment of the tile is inside the
+// matrix and 16-byte aligned (all tiles but a ragged last one); the two
+// forms are separate code so that no branch joins inside the k loop.
+template <bool VEC>
+__device__ __forceinline__ void head_tile(const HeadArgs& a, HeadSmem& sm) {
   const int N = a.N, D = a.D, V = a.V;
   const int v0 = blockIdx.x * kHeadCols, n0 = blockIdx.y * kHeadRows;
   const int tid = threadIdx.x, l = lane(), w = wave();
-  const int wn = w & 3, wv = w >> 2;
+  const int wn = w % kWavesN, wv = w / kWavesN;  // this wave's block of the tile
 
-  // global -> register staging: act row tid/2, 16 columns from (tid%2)*16
-  // (rows past N repeat row N-1; their results are not stored); W row
-  // tid/16 of the stage, 16 columns from (tid%16)*16 (rows past D are zero)
-  const float* ag = a.act + (size_t)min(n0 + (tid >> 1), N - 1) * a.lda + (tid & 1) * 16;
-  const int br = tid >> 4, bc = (tid & 15) * 16;
-  const bool bvec = v0 + kHeadCols <= V && (a.ldw & 3) == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15) == 0;
-  f32x4 pa[4], pb[4];
+  // global -> register staging, the same map for both tiles: stage row
+  // (tid / 64) + kStageRows j, 4 columns from (tid % 64) * 4, so that each wave moves
+  // one contiguous 1 KB row per load and per LDS store.  act is padded to
+  // whole tiles; W rows past D are read clamped and zeroed at the store.
+  const int sr = tid >> 6, sc = (tid & 63) * 4;
+  const float* ag = a.act + (size_t)sr * a.lda + n0 + sc;
+  // The loads only fill registers; what falls outside the matrix is zeroed
+  // when the registers go to LDS, so that no wait for the loads precedes
+  // the current stage's MFMAs.
+  f32x4 pa[kStagePasses], pb[kStagePasses];
   auto load = [&](int kb) {
     const int k0 = kb * kHeadK;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) pa[j] = *reinterpret_cast<const f32x4*>(ag + k0 + 4 * j);
-    const int kr = k0 + br;
-    const float* bg = a.w + (size_t)min(kr, D - 1) * a.ldw;
-    if (bvec) {
+    for (int j = 0; j < kStagePasses; ++j)
+      pa[j] = *reinterpret_cast<const f32x4*>(ag + (size_t)(k0 + kStageRows * j) * a.lda);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(bg + v0 + bc + 4 * j);
-        pb[j] = kr < D ? v : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < kStagePasses; ++j) {
+      const float* bg = a.w + (size_t)min(k0 + sr + kStageRows * j, D - 1) * a.ldw;
+      if constexpr (VEC) {
+        pb[j] = *reinterpret_cast<const f32x4*>(bg + v0 + sc);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pb[j][e] = bg[min(v0 + sc + e, V - 1)];
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int v = v0 + bc + 4 * j + e;
-          const float x = bg[min(v, V - 1)];
-          pb[j][e] = (kr < D && v < V) ? x : 0.0f;
-        }
     }
   };
-  auto store = [&](int buf) {
-    float* as = sm.a[buf] + (tid >> 1) * kAStride + (tid & 1) * 16;
+  auto store = [&](int kb, int buf, int j) {
+    {
+      const int r = sr + kStageRows * j;
+      *reinterpret_cast<f32x4*>(sm.a[buf] + r * kTileStride + sc) = pa[j];
+      const bool kin = kb * kHeadK + r < D;
+      f32x4 v = pb[j];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      *reinterpret_cast<f32x2*>(as + 4 * j) = f32x2{pa[j][0], pa[j][1]};
-      *reinterpret_cast<f32x2*>(as + 4 * j + 2) = f32x2{pa[j][2], pa[j][3]};
+      for (int e = 0; e < 4; ++e) v[e] = (kin && v0 + sc + e < V) ? v[e] : 0.0f;
+      *reinterpret_cast<f32x4*>(sm.b[buf] + r * kTileStride + sc) = v;
     }
-    float* bs = sm.b[buf] + br * kBStride + bc;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<f32x4*>(bs + 4 * j) = pb[j];
   };
 
-  f32x16 acc[2][4];
+  f32x16 acc[kMT][4];
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
@@ -115,52 +169,83 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   const int nkb = head_kpad(D) / kHeadK;
   load(0);
-  store(0);
+#pragma unroll
+  for (int j = 0; j < kStagePasses; ++j) store(0, 0, j);
   wg_barrier();
   for (int kb = 0; kb < nkb; ++kb) {
     const int cur = kb & 1;
     if (kb + 1 < nkb) load(kb + 1);
     // operands of v_mfma_f32_32x32x2_f32 at k step t: lane l holds
-    // A[row l%32][k 2t + l/32] and B[k 2t + l/32][column l%32]
-    const float* as = sm.a[cur] + (wn * 64 + (l & 31)) * kAStride + (l >> 5);
-    const float* bs = sm.b[cur] + (l >> 5) * kBStride + wv * 128 + (l & 31);
+    // A[row l%32][k 2t + l/32] and B[k 2t + l/32][column l%32]; both tiles
+    // are k-major, so each half-wave reads 32 consecutive floats
+    const float* as = sm.a[cur] + (l >> 5) * kTileStride + wn * 32 * kMT + (l & 31);
+    const float* bs = sm.b[cur] + (l >> 5) * kTileStride + wv * 128 + (l & 31);
+    // the operands of step t + kAhead are read from LDS while step t's
+    // MFMAs run
+    float fa[kAhead + 1][kMT], fb[kAhead + 1][4];
+    auto frags = [&](int t, int slot) {
+#pragma unroll
+      for (int i = 0; i < kMT; ++i) fa[slot][i] = as[2 * t * kTileStride + 32 * i];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) fb[slot][i] = bs[2 * t * kTileStride + 32 * i];
+    };
+#pragma unroll
+    for (int t = 0; t < kAhead; ++t) frags(t, t);
 #pragma unroll
     for (int t = 0; t < kHeadK / 2; ++t) {
-      const float fa0 = as[2 * t], fa1 = as[32 * kAStride + 2 * t];
-      float fb[4];
+      const int sl = t % (kAhead + 1);
+      if (t + kAhead < kHeadK / 2) frags(t + kAhead, (t + kAhead) % (kAhead + 1));
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) fb[nt] = bs[2 * t * kBStride + 32 * nt];
+      for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        acc[0][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa0, fb[nt], acc[0][nt], 0, 0, 0);
-        acc[1][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa1, fb[nt], acc[1][nt], 0, 0, 0);
-      }
+        for (int mt = 0; mt < kMT; ++mt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[sl][mt], fb[sl][nt], acc[mt][nt], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      // the next stage goes to the other LDS buffer (its last reads were
+      // before the previous barrier)
+      if (t >= kStoreStep && t < kStoreStep + kStagePasses && kb + 1 < nkb) store(kb + 1, cur ^ 1, t - kStoreStep);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (kb + 1 < nkb) store(cur ^ 1);
     wg_barrier();
   }
 
   // accumulator r of lane l holds row 8*(r/4) + 4*(l/32) + r%4, column l%32
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
       const int v = v0 + wv * 128 + nt * 32 + (l & 31);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int n = n0 + wn * 64 + mt * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+        const int n = n0 + wn * 32 * kMT + mt * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
         if (n < N && v < V) a.out[(size_t)n * a.ldo + v] = acc[mt][nt][r];
       }
     }
 }
 
-size_t head_ws_bytes(int N, int D) { return (size_t)N * head_kpad(D) * sizeof(float); }
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(kGemmWaves / 4, kGemmWaves / 4))) void
+k_head_gemm(HeadArgs a) {
+  __shared__ HeadSmem sm;
+  const int v0 = blockIdx.x * kHeadCols;
+  const bool vec = v0 + kHeadCols <= a.V && (a.ldw & 3) == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15) == 0;
+  if (vec) head_tile<true>(a, sm);
+  else head_tile<false>(a, sm);
+}
+
+size_t head_ws_bytes(int N, int D) {
+  return ((size_t)head_kpad(D) * head_npad(N) + (size_t)N) * sizeof(float) + 256;
+}
 
 hipError_t launch_head(HeadArgs a, hipStream_t s) {
-  a.lda = head_kpad(a.D);
-  hipLaunchKernelGGL(k_head_rmsnorm, dim3(a.N), dim3(kThreads), 0, s, a);
-  const dim3 grid((unsigned)((a.V + kHeadCols - 1) / kHeadCols), (unsigned)((a.N + kHeadRows - 1) / kHeadRows));
-  hipLaunchKernelGGL(k_head_gemm, grid, dim3(kThreads), 0, s, a);
+  // workspace: act [Dp][lda] (k-major), then rinv [N]
+  a.lda = head_npad(a.N);
+  a.rinv = a.act + (size_t)head_kpad(a.D) * a.lda;
+  hipLaunchKernelGGL(k_head_rms, dim3(a.N), dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL(k_head_act, dim3((unsigned)(head_kpad(a.D) / 32), (unsigned)(a.lda / 64)), dim3(kThreads), 0, s,
+                     a);
+  const dim3 grid((unsigned)((a.V + kHeadCols - 1) / kHeadCols), (unsigned)(a.lda / kHeadRows));
+  hipLaunchKernelGGL(k_head_gemm, grid, dim3(kGemmThreads), 0, s, a);
   return hipGetLastError();
 }
 

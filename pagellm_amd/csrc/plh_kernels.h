@@ -96,8 +96,9 @@ struct HeadArgs {
   int64_t ldw;
   float* out;         // [N, ldo] logits
   int64_t ldo;
-  float* act;         // workspace [N, lda]: normalised rows, zero-padded
+  float* act;         // workspace [Dp, lda]: normalised rows, k-major, zero-padded
   int64_t lda;
+  float* rinv;        // workspace [N]: 1 / rms of each row
   int N, D, V;
 };
 
