@@ -324,6 +324,8 @@ def main() -> None:
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the other workloads (zipf32k, zipf152k, char65, spec32k verify)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
+    ap.add_argument("--only", choices=["spec32k", "head128k"],
+                    help="run one of the other configurations alone and print its JSON (for profiling)")
     args = ap.parse_args()
 
     if args.cpu_baseline_child:
@@ -334,6 +336,10 @@ def main() -> None:
         return
     if args.pmc_probe:
         pmc_probe(args.workload)
+        return
+    if args.only:
+        fn = {"spec32k": bench_verify, "head128k": bench_head}[args.only]
+        print(json.dumps(fn(steps=min(args.steps, 50), warmup=min(args.warmup, 5))), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
