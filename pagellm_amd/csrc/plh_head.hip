@@ -16,9 +16,10 @@
 //                   Both operands are k-major in LDS (each half-wave reads
 //                   32 consecutive floats per MFMA operand); k streams
 //                   through LDS 32 at a time, double-buffered: the next
-//                   stage's global loads are in flight, and its LDS stores
-//                   trickle in, while the matrix cores work on the current
-//                   one.
+//                   stage is copied from HBM straight into LDS
+//                   (global_load_lds_dwordx4) while the matrix cores work on
+//                   the current one, and operand reads run two k steps ahead
+//                   of the MFMAs.
 #include "plh_device.h"
 #include "plh_kernels.h"
 
@@ -108,14 +109,20 @@ constexpr int kStagePasses = kHeadK / kStageRows;
 // after steps kStoreStep .. kStoreStep + kStagePasses - 1, so that LDS
 // writes never arrive as a burst in front of the operand reads.
 constexpr int kStoreStep = 1;
-constexpr int kAhead = 1;                        // k steps the operand reads run ahead
+constexpr int kAhead = 2;                        // k steps the operand reads run ahead
 static_assert(kStoreStep + kStagePasses <= kHeadK / 2, "stage stores must end inside the k loop");
 
 // One workgroup tile.  VEC: every W row segment of the tile is inside the
 // matrix and 16-byte aligned (all tiles but a ragged last one); the two
 // forms are separate code so that no branch joins inside the k loop.
-template <bool VEC>
+// DMA (full tiles whose k stages all lie inside D): the stages go from HBM
+// straight into LDS (global_load_lds_dwordx4: each wave's load fills one
+// contiguous 1 KB LDS row, lane l at 16 l), with no registers or LDS
+// stores on the way; the wave waits for its copies before the barrier that
+// ends the stage.
+template <bool VEC, bool DMA>
 __device__ __forceinline__ void head_tile(const HeadArgs& a, HeadSmem& sm) {
+  static_assert(!DMA || VEC, "the DMA form needs whole, aligned rows");
   const int N = a.N, D = a.D, V = a.V;
   const int v0 = blockIdx.x * kHeadCols, n0 = blockIdx.y * kHeadRows;
   const int tid = threadIdx.x, l = lane(), w = wave();
@@ -167,14 +174,38 @@ __device__ __forceinline__ void head_tile(const HeadArgs& a, HeadSmem& sm) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mt][nt][r] = 0.0f;
 
-  const int nkb = head_kpad(D) / kHeadK;
-  load(0);
+  // the DMA form: stage kb into LDS buffer buf (the LDS row of each copy is
+  // the same for the whole wave, as the instruction requires)
+  auto dma = [&](int kb, int buf) {
+    const int k0 = kb * kHeadK;
 #pragma unroll
-  for (int j = 0; j < kStagePasses; ++j) store(0, 0, j);
+    for (int j = 0; j < kStagePasses; ++j) {
+      const int r = sr + kStageRows * j;
+      __builtin_amdgcn_global_load_lds(ag + (size_t)(k0 + kStageRows * j) * a.lda, sm.a[buf] + r * kTileStride, 16,
+                                       0, 0);
+      __builtin_amdgcn_global_load_lds(a.w + (size_t)(k0 + r) * a.ldw + v0 + sc, sm.b[buf] + r * kTileStride, 16, 0,
+                                       0);
+    }
+  };
+  auto dma_wait = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
+
+  const int nkb = head_kpad(D) / kHeadK;
+  if constexpr (DMA) {
+    dma(0, 0);
+    dma_wait();
+  } else {
+    load(0);
+#pragma unroll
+    for (int j = 0; j < kStagePasses; ++j) store(0, 0, j);
+  }
   wg_barrier();
   for (int kb = 0; kb < nkb; ++kb) {
     const int cur = kb & 1;
-    if (kb + 1 < nkb) load(kb + 1);
+    if constexpr (DMA) {
+      if (kb + 1 < nkb) dma(kb + 1, cur ^ 1);  // the other buffer's last reads were before the barrier
+    } else {
+      if (kb + 1 < nkb) load(kb + 1);
+    }
     // operands of v_mfma_f32_32x32x2_f32 at k step t: lane l holds
     // A[row l%32][k 2t + l/32] and B[k 2t + l/32][column l%32]; both tiles
     // are k-major, so each half-wave reads 32 consecutive floats
@@ -204,9 +235,13 @@ __device__ __forceinline__ void head_tile(const HeadArgs& a, HeadSmem& sm) {
       __builtin_amdgcn_sched_barrier(0);
       // the next stage goes to the other LDS buffer (its last reads were
       // before the previous barrier)
-      if (t >= kStoreStep && t < kStoreStep + kStagePasses && kb + 1 < nkb) store(kb + 1, cur ^ 1, t - kStoreStep);
+      if constexpr (!DMA) {
+        if (t >= kStoreStep && t < kStoreStep + kStagePasses && kb + 1 < nkb)
+          store(kb + 1, cur ^ 1, t - kStoreStep);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (DMA) dma_wait();
     wg_barrier();
   }
 
@@ -229,8 +264,9 @@ k_head_gemm(HeadArgs a) {
   __shared__ HeadSmem sm;
   const int v0 = blockIdx.x * kHeadCols;
   const bool vec = v0 + kHeadCols <= a.V && (a.ldw & 3) == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15) == 0;
-  if (vec) head_tile<true>(a, sm);
-  else head_tile<false>(a, sm);
+  if (vec && a.D % kHeadK == 0) head_tile<true, true>(a, sm);
+  else if (vec) head_tile<true, false>(a, sm);
+  else head_tile<false, false>(a, sm);
 }
 
 size_t head_ws_bytes(int N, int D) {
