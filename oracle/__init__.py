@@ -1,7 +1,7 @@
 """CPU oracle for the pagellm sampler and logits producer: test infrastructure only.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import this package, and only as the checker or as the timed
+``bench.py`` may import this package, and only as the reference results or as the timed
 CPU baseline.  The product path (``pagellm_amd``) never imports it.
 """
 

@@ -1,6 +1,6 @@
 """CPU oracle for the logits producer: test infrastructure only.
 
-TEST INFRASTRUCTURE ONLY: the checker for ``plh_rmsnorm_lm_head``; the
+TEST INFRASTRUCTURE ONLY: the expected results for ``plh_rmsnorm_lm_head``; the
 product never imports it.
 
 A numpy restatement of the model's last two operations,

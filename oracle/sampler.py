@@ -1,6 +1,6 @@
 """CPU oracle: a numpy restatement of pagellm's sampler and speculative verify.
 
-TEST INFRASTRUCTURE ONLY.  This module is the checker for the HIP sampler in
+TEST INFRASTRUCTURE ONLY.  This module gives the expected results for the HIP sampler in
 ``pagellm_amd`` and the timed CPU baseline in ``bench.py``; the product never
 imports it.
 
