@@ -123,8 +123,9 @@ def pmc_probe(workload: str) -> None:
     print("pmc probe done", flush=True)
 
 
-def traffic_from(workload: str, fetch_dir: str, write_dir: str) -> None:
-    """HBM bytes per k_sample_chunks launch from the two counter runs."""
+def traffic_from(workload: str, fetch_dir: str, write_dir: str, dst: Path | None = None) -> dict:
+    """HBM bytes per k_sample_chunks launch from the two counter runs,
+    written to profiles/traffic_<workload>.json (or dst)."""
     import csv
 
     def per_kernel(folder: str, counter: str):
@@ -154,9 +155,10 @@ def traffic_from(workload: str, fetch_dir: str, write_dir: str) -> None:
     out = {"workload": workload, "kernel": "k_sample_chunks",
            "bytes_per_launch": res["FETCH_SIZE"]["bytes_per_launch"] + res["WRITE_SIZE"]["bytes_per_launch"],
            "algorithmic_bytes": workloads.algorithmic_bytes(w), "counters": res}
-    dst = ROOT / "profiles" / f"traffic_{workload}.json"
+    dst = dst if dst is not None else ROOT / "profiles" / f"traffic_{workload}.json"
     dst.write_text(json.dumps(out, indent=1) + "\n")
     print(json.dumps(out))
+    return out
 
 
 def bench_config(name: str, steps: int = 20, warmup: int = 3) -> dict:

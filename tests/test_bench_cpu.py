@@ -1,0 +1,66 @@
+"""bench.py's contract pieces that need no GPU: the one-GPU guard, the
+counter-run arithmetic behind roofline.traffic, and the algorithmic bytes
+the roofline prices."""
+
+from __future__ import annotations
+
+import csv
+import subprocess
+import sys
+
+import pytest
+
+from conftest import ROOT
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def _counter_csv(folder, counter, rows):
+    folder.mkdir(parents=True)
+    with open(folder / "run_counter_collection.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+        w.writeheader()
+        for did, name, value in rows:
+            # counters come split over the chip's blocks: two rows per dispatch
+            w.writerow({"Dispatch_Id": did, "Kernel_Name": name, "Counter_Name": counter, "Counter_Value": value / 2})
+            w.writerow({"Dispatch_Id": did, "Kernel_Name": name, "Counter_Name": counter, "Counter_Value": value / 2})
+
+
+def test_traffic_scaling_from_counter_runs(tmp_path):
+    import bench
+
+    copy_bytes = bench.COPY_BYTES
+    # FETCH_SIZE reads half the copy's bytes (scale 2); WRITE_SIZE all of them
+    _counter_csv(tmp_path / "f", "FETCH_SIZE", [
+        (1, "__amd_rocclr_copyBuffer", copy_bytes / 1024 / 2),
+        (2, "void plh::k_sample_chunks<float, true>(plh::SampleArgs)", 1000.0),
+        (3, "void plh::k_sample_chunks<float, true>(plh::SampleArgs)", 3000.0),
+        (4, "void plh::k_sample_final<float, true>(plh::SampleArgs)", 99999.0),
+    ])
+    _counter_csv(tmp_path / "w", "WRITE_SIZE", [
+        (1, "__amd_rocclr_copyBuffer", copy_bytes / 1024),
+        (2, "void plh::k_sample_chunks<float, true>(plh::SampleArgs)", 10.0),
+        (3, "void plh::k_sample_chunks<float, true>(plh::SampleArgs)", 30.0),
+    ])
+    out = bench.traffic_from("char65", str(tmp_path / "f"), str(tmp_path / "w"), dst=tmp_path / "t.json")
+    f, w = out["counters"]["FETCH_SIZE"], out["counters"]["WRITE_SIZE"]
+    assert f["scale"] == pytest.approx(2.0) and w["scale"] == pytest.approx(1.0)
+    assert f["kib_per_launch"] == pytest.approx(2000.0) and w["kib_per_launch"] == pytest.approx(20.0)
+    assert out["bytes_per_launch"] == pytest.approx(2000.0 * 1024 * 2 + 20.0 * 1024)
+    assert (tmp_path / "t.json").exists()
+
+
+def test_algorithmic_bytes_of_the_headline_workload():
+    """4V per row of fp32 logits, 4H per history id of a penalised row, 48
+    per row of parameters, uniform, offset and id."""
+    from pagellm_amd import workloads
+
+    w = workloads.mixed128k()
+    B, V = w["logits"].shape
+    pen_ids = sum(len(c) for c, p in zip(w["contexts"], w["params"]) if p.repetition_penalty != 1.0)
+    assert workloads.algorithmic_bytes(w) == 4 * B * V + 4 * pen_ids + 48 * B == 131_870_720
