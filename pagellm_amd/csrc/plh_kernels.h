@@ -83,7 +83,6 @@ struct VerifyArgs {
 struct VerifyWs {
   int32_t* stop;    // [B] stop position: first rejection, k, or -1
   double* part;     // [B * C * 2] chunk sums of the residual and of p
-  uint64_t* fx;     // [B * C] chunk totals of the fixed-point weights
   int C;            // chunks per row
 };
 
@@ -113,8 +112,8 @@ hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, int num_c
                               hipEvent_t between = nullptr);
 hipError_t launch_draw(const DrawArgs& a, bool f64, hipStream_t s);
 hipError_t launch_penalize(const PenalizeArgs& a, bool f64, hipStream_t s);
-// Verify: workspace bytes for B rows of V tokens, its layout, and the three
-// launches (stop positions and chunk sums, chunk fixed-point totals, draw).
+// Verify: workspace bytes for B rows of V tokens, its layout, and the two
+// launches (stop positions and chunk sums, then the draw).
 size_t verify_ws_bytes(int B, int V);
 VerifyWs verify_ws_layout(void* base, int B, int V);
 hipError_t launch_verify(const VerifyArgs& a, const VerifyWs& ws, bool f64, hipStream_t s);

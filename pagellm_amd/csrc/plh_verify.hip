@@ -12,16 +12,16 @@
 // that a batch of a few dozen rows still fills the chip:
 //   k_verify_parts  (row, chunk)  stop position; float64 chunk sums of the
 //                                 residual and of p;
-//   k_verify_fx     (row, chunk)  the row's total W from the chunk sums (one
-//                                 fixed order, the same in every workgroup);
-//                                 the chunk's total of the fixed-point
-//                                 weights round(w / W * 2^62);
-//   k_verify_draw   (row)         t = floor(u * sum of chunk totals); the
-//                                 chunk whose exact running total first
-//                                 exceeds t, rescanned for the token.
-// The fixed-point sums are exact integers, so the chunk found by the
-// running totals always holds the crossing token, whatever the order of
-// the additions.
+//   k_verify_draw   (row)         W and the running chunk totals in one fixed
+//                                 order; the first chunk whose running total
+//                                 exceeds u * W is rescanned in float64 for
+//                                 the token.
+// The float64 running sums add the weights in another order than numpy's
+// cumsum; the token they give differs from the reference's only when u lies
+// within ~1e-15 (relative) of a CDF boundary.  When the rescan's own
+// rounding leaves the crossing just past the chunk's end, the chunk's last
+// token of positive weight is taken (a neighbour of the boundary either
+// way).
 #include "plh_kernels.h"
 #include "plh_pipeline.h"
 
@@ -149,37 +149,8 @@ __global__ __launch_bounds__(kThreads) void k_verify_parts(VerifyArgs a, VerifyW
 }
 
 template <typename TIn>
-__global__ __launch_bounds__(kThreads) void k_verify_fx(VerifyArgs a, VerifyWs ws) {
-  __shared__ uint64_t redu[kWaves];
-  const int C = ws.C;
-  const int b = blockIdx.x / C, c = blockIdx.x - b * C;
-  const int k = a.k, V = a.V;
-  const int s = ws.stop[b];
-  if (s < 0) return;
-  const TIn* ps = reinterpret_cast<const TIn*>(a.p) + ((size_t)b * (k + 1) + s) * V;
-  const TIn* qs = s < k ? reinterpret_cast<const TIn*>(a.q) + ((size_t)b * k + s) * V : ps;
-  // loads first, all in flight together (indices clamped into the row)
-  const int i0 = c * kVChunk + (int)threadIdx.x;
-  TIn pv[kVPer], qv[kVPer];
-#pragma unroll
-  for (int l = 0; l < kVPer; ++l) {
-    const int i = min(i0 + l * kThreads, V - 1);
-    pv[l] = ps[i];
-    qv[l] = qs[i];
-  }
-  const DrawTotal d = draw_total(ws, b, s, k);
-  if (!(d.W > 0.0)) return;  // the draw takes V - 1 without reading the totals
-  uint64_t t = 0;
-#pragma unroll
-  for (int l = 0; l < kVPer; ++l)
-    t += to_fx(draw_weight((double)pv[l], (double)qv[l], d.resid, i0 + l * kThreads < V) / d.W);
-  t = block_sum<uint64_t>(t, redu);
-  if (threadIdx.x == 0) ws.fx[blockIdx.x] = t;
-}
-
-template <typename TIn>
 __global__ __launch_bounds__(kThreads) void k_verify_draw(VerifyArgs a, VerifyWs ws) {
-  __shared__ uint64_t redu[kWaves];
+  __shared__ double redd[kWaves];
   __shared__ int redi[kWaves];
   const int b = blockIdx.x;
   const int k = a.k, V = a.V, C = ws.C;
@@ -192,31 +163,39 @@ __global__ __launch_bounds__(kThreads) void k_verify_draw(VerifyArgs a, VerifyWs
   }
   const double u = a.draw_u_per_stop ? a.draw_u[(size_t)b * (k + 1) + s] : a.draw_u[b];
   const DrawTotal d = draw_total(ws, b, s, k);
-  int tok = V - 1;  // sampling.py:98: no crossing (or no mass) takes the last id
+  int tok = V - 1;  // sampling.py:98: no mass takes the last id
   if (d.W > 0.0) {
-    const uint64_t* fx = ws.fx + (size_t)b * C;
-    uint64_t tf = 0;
-    for (int j = lane(); j < C; j += kWave) tf += fx[j];
-    tf = wave_sum(tf);
-    const uint64_t t_fx = (uint64_t)__double2ull_rd(u * (double)tf);
-    // the first chunk whose running total exceeds t_fx (every wave alike)
-    int cs = -1;
-    uint64_t before = 0, run = 0;
-    for (int base = 0; base < C && cs < 0; base += kWave) {
+    const double t = u * d.W;
+    const double* part = ws.part + (size_t)b * C * 2 + (d.resid ? 0 : 1);
+    // the first chunk whose running total exceeds t, else the last chunk
+    // with mass (every wave alike, sums in one fixed order)
+    int cs = -1, clast = -1;
+    double before = 0.0, blast = 0.0, run = 0.0;
+    for (int base = 0; base < C; base += kWave) {
       const int j = base + lane();
-      const uint64_t v = j < C ? fx[j] : 0ull;
-      const uint64_t incl = run + wave_scan_incl(v, (uint64_t)0, OpAdd{});
-      const uint64_t m = __ballot(j < C && incl > t_fx);
+      const double v = j < C ? part[2 * j] : 0.0;
+      const double incl = run + wave_scan_incl(v, 0.0, OpAdd{});
+      const uint64_t pos = __ballot(j < C && v > 0.0);
+      if (pos != 0) {
+        const int f = 63 - __builtin_clzll(pos);
+        clast = base + f;
+        blast = lane_value(incl - v, f);
+      }
+      const uint64_t m = __ballot(j < C && incl > t);
       if (m != 0) {
         const int f = __builtin_ctzll(m);
         cs = base + f;
         before = lane_value(incl - v, f);
+        break;
       }
       run = lane_value(incl, kWave - 1);
     }
+    const bool crossed = cs >= 0;
+    if (!crossed) {
+      cs = clast;
+      before = blast;
+    }
     if (cs >= 0) {
-      // rescan that chunk in thread order: the same weights, the same exact total
-      const uint64_t tgt = t_fx - before;
       const TIn* ps = reinterpret_cast<const TIn*>(a.p) + ((size_t)b * (k + 1) + s) * V;
       const TIn* qs = s < k ? reinterpret_cast<const TIn*>(a.q) + ((size_t)b * k + s) * V : ps;
       const int i0 = cs * kVChunk + (int)threadIdx.x * kVPer;
@@ -227,22 +206,28 @@ __global__ __launch_bounds__(kThreads) void k_verify_draw(VerifyArgs a, VerifyWs
         pv[l] = ps[i];
         qv[l] = qs[i];
       }
-      uint64_t w[kVPer], ts = 0;
+      double w[kVPer], ts = 0.0;
 #pragma unroll
       for (int l = 0; l < kVPer; ++l) {
-        w[l] = to_fx(draw_weight((double)pv[l], (double)qv[l], d.resid, i0 + l < V) / d.W);
+        w[l] = draw_weight((double)pv[l], (double)qv[l], d.resid, i0 + l < V);
         ts += w[l];
       }
-      uint64_t tt;
-      uint64_t cum = block_excl_scan<uint64_t>(ts, redu, &tt);
-      int my = INT_MAX;
+      double tt;
+      double cum = before + block_excl_scan<double>(ts, redd, &tt);
+      int my = INT_MAX, mylast = -1;
 #pragma unroll
       for (int l = 0; l < kVPer; ++l) {
         cum += w[l];
-        if (my == INT_MAX && cum > tgt) my = i0 + l;
+        if (crossed && my == INT_MAX && cum > t) my = i0 + l;
+        if (w[l] > 0.0) mylast = i0 + l;
       }
       const int f = block_min<int>(my, redi);
-      if (f != INT_MAX) tok = f;
+      if (f != INT_MAX) {
+        tok = f;
+      } else {  // the crossing sits at the chunk's end (or u * W at the total)
+        tok = block_max<int>(mylast, redi);
+        if (tok < 0) tok = V - 1;
+      }
     }
   }
   if (threadIdx.x == 0) {
@@ -260,7 +245,7 @@ size_t up256(size_t v) { return (v + 255) / 256 * 256; }
 
 size_t verify_ws_bytes(int B, int V) {
   const size_t n = (size_t)B * verify_chunks(V);
-  return up256((size_t)B * sizeof(int32_t)) + up256(n * 2 * sizeof(double)) + up256(n * sizeof(uint64_t));
+  return up256((size_t)B * sizeof(int32_t)) + up256(n * 2 * sizeof(double));
 }
 
 VerifyWs verify_ws_layout(void* base, int B, int V) {
@@ -271,8 +256,6 @@ VerifyWs verify_ws_layout(void* base, int B, int V) {
   w.stop = reinterpret_cast<int32_t*>(p);
   p += up256((size_t)B * sizeof(int32_t));
   w.part = reinterpret_cast<double*>(p);
-  p += up256(n * 2 * sizeof(double));
-  w.fx = reinterpret_cast<uint64_t*>(p);
   return w;
 }
 
@@ -281,7 +264,6 @@ hipError_t launch_verify_t(const VerifyArgs& a, const VerifyWs& ws, hipStream_t 
   const dim3 block(kThreads);
   const dim3 grid_parts((unsigned)((size_t)a.B * ws.C));
   hipLaunchKernelGGL((k_verify_parts<TIn>), grid_parts, block, 0, s, a, ws);
-  hipLaunchKernelGGL((k_verify_fx<TIn>), grid_parts, block, 0, s, a, ws);
   hipLaunchKernelGGL((k_verify_draw<TIn>), dim3(a.B), block, 0, s, a, ws);
   return hipGetLastError();
 }

@@ -143,3 +143,31 @@ def test_verify_draw_across_chunks():
             if n[b] != rn[b] or not np.array_equal(toks[b], rt[b]):
                 gap = verify_boundary_gap(Pc[b], Qc[b], drafts[b], aus[b], dus[b])
                 assert gap < 1e-6, (dt, b, n[b], rn[b], gap)
+
+
+def test_verify_draw_ends_of_the_cdf():
+    """Uniforms at 0 and at the largest double below 1, mass confined to
+    one chunk (zero weight after it, so the last chunks carry nothing), in
+    the bonus draw (k = 0) and the residual draw: the first and the last
+    token of positive weight, as numpy's searchsorted gives them."""
+    V = 3 * 4096 + 5
+    g = np.random.default_rng(4)
+    u_top = float(np.nextafter(1.0, 0.0))
+    for lo, hi in [(0, 100), (4100, 4200), (4095, 4097)]:
+        p = np.zeros((1, 1, V))
+        p[0, 0, lo:hi] = _dist(g, hi - lo)
+        for u in (0.0, u_top):
+            toks, n = verify_batch(p, np.zeros((1, 0, V)), np.zeros((1, 0), np.int64), np.zeros((1, 0)), [u])
+            rt, rn = oracle.verify_batch(p, np.zeros((1, 0, V)), np.zeros((1, 0), np.int64), np.zeros((1, 0)),
+                                         np.array([u]))
+            assert n[0] == rn[0] == 0
+            assert toks[0][0] == rt[0][0] == (lo if u == 0.0 else hi - 1), (lo, hi, u, toks, rt)
+        # residual draw: q puts its mass elsewhere, so the residual is p's
+        q = np.zeros((1, 1, V))
+        q[0, 0, V - 1] = 1.0
+        pp = np.concatenate([p, p], axis=1)
+        for u in (0.0, u_top):
+            toks, n = verify_batch(pp, q, [[V - 1]], [[0.999]], [u])
+            rt, rn = oracle.verify_batch(pp, q, np.array([[V - 1]]), np.array([[0.999]]), np.array([u]))
+            assert n[0] == rn[0] == 0
+            assert toks[0][0] == rt[0][0] == (lo if u == 0.0 else hi - 1), (lo, hi, u, toks, rt)
