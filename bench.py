@@ -301,6 +301,57 @@ def bench_head(steps: int = 20, warmup: int = 3, N: int = 256, D: int = 4096, V:
     return res
 
 
+def copy_bandwidth(nbytes: int = 1 << 30, reps: int = 10) -> float:
+    """GB/s of a plain device-to-device copy (bytes read + bytes written per
+    second): the secondary, measured denominator beside the 8 TB/s peak."""
+    import torch
+
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    gbps = 2.0 * nbytes * reps / (a.elapsed_time(b) * 1e-3) / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    return gbps
+
+
+def bench_end_to_end(w, logits, steps: int = 50, warmup: int = 5) -> dict:
+    """Host-inclusive time per step of the engine adapter with the logits
+    already in HBM: each step uploads the per-row parameters, uniforms and
+    history spans from the host, runs the sampler, appends the ids to the
+    device-resident histories and downloads the ids (wall clock, one host
+    thread, the download waits for the step)."""
+    import numpy as np
+
+    from pagellm_amd import _native
+    from pagellm_amd.engine import BatchSampler, DeviceHistories
+
+    B, V = w["logits"].shape
+    H = max(len(c) for c in w["contexts"])
+    hist = DeviceHistories(V, B, H + warmup + steps + 1, ctx=_native.Context(0))
+    for b in range(B):
+        hist.add(b, np.asarray(w["contexts"][b]))
+    sampler = BatchSampler(hist)
+    keys = list(range(B))
+    u = w["uniforms"]
+    for _ in range(warmup):
+        sampler.sample(logits, w["params"], None, keys, uniforms=u)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ids = sampler.sample(logits, w["params"], None, keys, uniforms=u)
+    dt = (time.perf_counter() - t0) / steps
+    hist.ctx.close()
+    return {"us_per_step": dt * 1e6, "rows_per_s": B / dt, "steps": steps, "ids_checked": int(ids.shape[0])}
+
+
 def load_traffic(workload: str):
     f = ROOT / "profiles" / f"traffic_{workload}.json"
     if f.exists():
@@ -412,6 +463,10 @@ def main() -> None:
     rows_per_s = B / (ms * 1e-3)
     gbps = algo_bytes / (ms * 1e-3) / 1e9
     kernel_gbps = algo_bytes / (kernel_ms * 1e-3) / 1e9 if calls else None
+    print("[bench] end to end (engine adapter, host in the loop)", file=sys.stderr, flush=True)
+    e2e = bench_end_to_end(w, logits[0])
+    print("[bench] copy bandwidth", file=sys.stderr, flush=True)
+    copy_gbps = copy_bandwidth()
     others = None
     if not args.no_other_configs:
         others = {}
@@ -445,7 +500,9 @@ def main() -> None:
         "fallback_rows_per_step": fallback,
         "roofline": {"bound": "hbm", "achieved": kernel_gbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": kernel_gbps / PEAK_HBM_GBPS if kernel_gbps else None,
-                     "traffic": load_traffic(args.workload), "kernel": "k_sample_chunks"},
+                     "traffic": load_traffic(args.workload), "kernel": "k_sample_chunks",
+                     "copy_gbps": copy_gbps, "frac_of_copy": kernel_gbps / copy_gbps if kernel_gbps else None},
+        "end_to_end": e2e,
         "cpu_baseline": cpu,
         "other_configs": others,
     }

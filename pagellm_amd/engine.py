@@ -94,24 +94,28 @@ class DeviceHistories:
                                    out.nbytes))
         return out
 
+    def _slots_lengths(self, keys: Sequence) -> tuple[np.ndarray, np.ndarray]:
+        B = len(keys)
+        slots = np.fromiter(map(self._slot.__getitem__, keys), dtype=np.int64, count=B)
+        lens = np.fromiter(map(self._len.__getitem__, keys), dtype=np.int64, count=B)
+        return slots, lens
+
     def spans(self, keys: Sequence, active: Sequence[bool]) -> np.ndarray:
         """int64 [2B] (start, end) per row; inactive rows get an empty span."""
-        sp = np.zeros(2 * len(keys), dtype=np.int64)
-        for b, key in enumerate(keys):
-            start = self._slot[key] * self.max_len
-            sp[2 * b] = start
-            sp[2 * b + 1] = start + (self._len[key] if active[b] else 0)
+        slots, lens = self._slots_lengths(keys)
+        sp = np.empty(2 * len(keys), dtype=np.int64)
+        sp[0::2] = slots * self.max_len
+        sp[1::2] = sp[0::2] + np.where(np.asarray(active, dtype=bool), lens, 0)
         return sp
 
     def append_positions(self, keys: Sequence) -> np.ndarray:
         """int64 [B]: where each row's next id goes."""
-        pos = np.empty(len(keys), dtype=np.int64)
-        for b, key in enumerate(keys):
-            n = self._len[key]
-            if n >= self.max_len:
-                raise RuntimeError(f"history of {key!r} is full ({self.max_len} tokens)")
-            pos[b] = self._slot[key] * self.max_len + n
-        return pos
+        slots, lens = self._slots_lengths(keys)
+        full = lens >= self.max_len
+        if full.any():
+            key = keys[int(np.argmax(full))]
+            raise RuntimeError(f"history of {key!r} is full ({self.max_len} tokens)")
+        return slots * self.max_len + lens
 
     def advance(self, keys: Sequence) -> None:
         for key in keys:
@@ -125,6 +129,9 @@ class BatchSampler:
     def __init__(self, histories: DeviceHistories):
         self.hist = histories
         self.ctx = histories.ctx
+        # the last step's packed parameters, with references to its
+        # SamplingParams objects (so that equal ids mean the same objects)
+        self._packed = None
 
     def sample(self, logits, params, rngs: Sequence | None, keys: Sequence, *, uniforms=None) -> np.ndarray:
         """Samples one token per row and appends it to the row's history.
@@ -166,22 +173,28 @@ class BatchSampler:
         params = _expand_params(params, B)
         u = (np.asarray(uniforms, dtype=np.float64).reshape(B) if uniforms is not None
              else _draw_uniforms(params, rngs, B))
-        t, k, p, r = _pack_params(params)
+        ids = list(map(id, params))
+        if self._packed is not None and self._packed[0] == ids:
+            t, k, p, r = self._packed[2]  # the same requests in the same rows as the last step
+        else:
+            t, k, p, r = _pack_params(params)
+            self._packed = (ids, list(params), (t, k, p, r))
         # sampling.py:56: only rows whose penalty is active read their history
-        spans = self.hist.spans(keys, [sp.repetition_penalty != 1.0 for sp in params])
+        spans = self.hist.spans(keys, r != 1.0)
         pos = self.hist.append_positions(keys)
-        d_t = c.scratch_upload("eng_t", t)
-        d_k = c.scratch_upload("eng_k", k)
-        d_p = c.scratch_upload("eng_p", p)
-        d_r = c.scratch_upload("eng_r", r)
-        d_u = c.scratch_upload("eng_u", u)
-        d_sp = c.scratch_upload("eng_spans", spans)
-        d_pos = c.scratch_upload("eng_pos", pos)
+        # every per-row array in one host buffer, one copy to the device
+        parts = [t, p, r, u, spans, pos, k]
+        offs = np.cumsum([0] + [a.nbytes for a in parts])
+        stage = np.empty(int(offs[-1]), dtype=np.uint8)
+        for a, o in zip(parts, offs[:-1]):
+            stage[o:o + a.nbytes] = np.ascontiguousarray(a).view(np.uint8)
+        d = c.scratch_upload("eng_stage", stage)
+        d_t, d_p, d_r, d_u, d_sp, d_pos, d_k = (d.ptr + int(o) for o in offs[:-1])
         out = c.scratch("eng_out", (B,), np.int32)
-        c.sample(ptr, code, ld, B, V, self.hist.slab.ptr, d_sp.ptr, d_t.ptr, d_k.ptr, d_p.ptr, d_r.ptr, d_u.ptr,
+        c.sample(ptr, code, ld, B, V, self.hist.slab.ptr, d_sp, d_t, d_k, d_p, d_r, d_u,
                  out.ptr, None, _native.PLH_SAMPLE_HIST_SPANS)
         # llm_engine.py:284: the token joins the history, on the device
-        c.append_ids(self.hist.slab.ptr, d_pos.ptr, out.ptr, B)
+        c.append_ids(self.hist.slab.ptr, d_pos, out.ptr, B)
         ids = out.download().astype(np.int64)
         self.hist.advance(keys)
         return ids

@@ -84,17 +84,27 @@ def _pack_histories(contexts, params: Sequence[SamplingParams], B: int, V: int):
 
 
 def _pack_params(params: Sequence[SamplingParams]):
+    """The per-row parameter arrays (float64 T, int32 top_k clamped to
+    2^31 - 1, float64 top_p and penalty).  A batch usually holds few
+    distinct SamplingParams objects (one per request); each distinct object
+    is then read once and the rows index into its values."""
     B = len(params)
-    t = np.empty(B, dtype=np.float64)
-    k = np.empty(B, dtype=np.int32)
-    p = np.empty(B, dtype=np.float64)
-    r = np.empty(B, dtype=np.float64)
-    for b, sp in enumerate(params):
-        t[b] = sp.temperature
-        k[b] = min(int(sp.top_k), 2**31 - 1)
-        p[b] = sp.top_p
-        r[b] = sp.repetition_penalty
-    return t, k, p, r
+    ids = list(map(id, params))
+    first = dict.fromkeys(ids)
+    if 4 * len(first) <= B:
+        by_id = dict(zip(ids, params))
+        objs = [by_id[key] for key in first]
+        pos = {key: i for i, key in enumerate(first)}
+        idx = np.fromiter(map(pos.__getitem__, ids), dtype=np.intp, count=B)
+    else:
+        objs, idx = params, None
+    t = np.array([sp.temperature for sp in objs], dtype=np.float64)
+    k = np.array([min(int(sp.top_k), 2**31 - 1) for sp in objs], dtype=np.int32)
+    p = np.array([sp.top_p for sp in objs], dtype=np.float64)
+    r = np.array([sp.repetition_penalty for sp in objs], dtype=np.float64)
+    if idx is None:
+        return t, k, p, r
+    return t[idx], k[idx], p[idx], r[idx]
 
 
 def _expand_params(params, B: int) -> list[SamplingParams]:
