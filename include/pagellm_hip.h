@@ -82,6 +82,16 @@ int plh_alloc(plh_ctx* ctx, void** out, size_t bytes);
 int plh_free(plh_ctx* ctx, void* ptr);
 int plh_h2d(plh_ctx* ctx, void* dst, const void* src, size_t bytes);
 int plh_d2h(plh_ctx* ctx, void* dst, const void* src, size_t bytes);
+
+/* Page-locked host memory, and a host-to-device copy that is only queued on
+ * the context's stream (no wait): src must stay unchanged until the stream
+ * has passed the copy, e.g. until the next plh_d2h or plh_sync returns.
+ * For the small per-step inputs of a serving loop (one copy per step from
+ * one page-locked buffer).  No reference counterpart (the reference's
+ * inputs never leave the host). */
+int plh_host_alloc(plh_ctx* ctx, void** out, size_t bytes);
+int plh_host_free(plh_ctx* ctx, void* ptr);
+int plh_h2d_async(plh_ctx* ctx, void* dst, const void* src, size_t bytes);
 int plh_sync(plh_ctx* ctx);
 
 /*

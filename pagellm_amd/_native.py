@@ -45,6 +45,9 @@ SIGNATURES = {
     "plh_free": (_c_int, [_vp, _vp]),
     "plh_h2d": (_c_int, [_vp, _vp, _vp, _c_sz]),
     "plh_d2h": (_c_int, [_vp, _vp, _vp, _c_sz]),
+    "plh_host_alloc": (_c_int, [_vp, ctypes.POINTER(_vp), _c_sz]),
+    "plh_host_free": (_c_int, [_vp, _vp]),
+    "plh_h2d_async": (_c_int, [_vp, _vp, _vp, _c_sz]),
     "plh_sync": (_c_int, [_vp]),
     "plh_sample": (
         _c_int,
@@ -172,6 +175,7 @@ class Context:
         self.handle = h.value
         self.device = device
         self._scratch: dict[str, DeviceArray] = {}
+        self._pinned: dict[str, tuple[int, int]] = {}
 
     def _check(self, rc: int) -> None:
         if rc != PLH_OK:
@@ -182,6 +186,10 @@ class Context:
         for buf in self._scratch.values():
             buf.free()
         self._scratch.clear()
+        if self.handle:
+            for ptr, _ in self._pinned.values():
+                self.lib.plh_host_free(self.handle, ptr)
+        self._pinned.clear()
         if self.handle:
             self.lib.plh_destroy(self.handle)
             self.handle = None
@@ -220,6 +228,26 @@ class Context:
     def scratch_upload(self, name: str, host) -> DeviceArray:
         host = np.ascontiguousarray(host)
         return self.scratch(name, host.shape, host.dtype).upload(host)
+
+    def pinned(self, name: str, nbytes: int) -> np.ndarray:
+        """A reusable page-locked host buffer (uint8, at least nbytes), for
+        plh_h2d_async; grown on demand."""
+        buf = self._pinned.get(name)
+        if buf is None or buf[1] < nbytes:
+            if buf is not None:
+                self._check(self.lib.plh_host_free(self.handle, buf[0]))
+            cap = max(int(nbytes), 4096)
+            ptr = _vp()
+            self._check(self.lib.plh_host_alloc(self.handle, ctypes.byref(ptr), cap))
+            buf = (ptr.value, cap)
+            self._pinned[name] = buf
+        return np.ctypeslib.as_array((ctypes.c_uint8 * buf[1]).from_address(buf[0]))
+
+    def h2d_async(self, dst_ptr: int, src: np.ndarray) -> None:
+        """Queue a copy of src (page-locked: from pinned()) to the device on
+        the context's stream; src must stay unchanged until the stream has
+        passed it (the next download or sync)."""
+        self._check(self.lib.plh_h2d_async(self.handle, dst_ptr, src.ctypes.data, src.nbytes))
 
     def sync(self) -> None:
         self._check(self.lib.plh_sync(self.handle))

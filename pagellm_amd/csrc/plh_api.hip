@@ -223,6 +223,38 @@ int plh_h2d(plh_ctx* c, void* dst, const void* src, size_t bytes) {
   return PLH_OK;
 }
 
+int plh_host_alloc(plh_ctx* c, void** out, size_t bytes) {
+  if (c == nullptr || out == nullptr) return PLH_ERR_INVALID_ARG;
+  *out = nullptr;
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  const hipError_t e = hipHostMalloc(out, bytes > 0 ? bytes : 1, hipHostMallocDefault);
+  if (e != hipSuccess) {
+    *out = nullptr;
+    return hip_fail(c, e, "hipHostMalloc");
+  }
+  return PLH_OK;
+}
+
+int plh_host_free(plh_ctx* c, void* p) {
+  if (c == nullptr) return PLH_ERR_INVALID_ARG;
+  if (p == nullptr) return PLH_OK;
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  PLH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  PLH_HIP(c, hipHostFree(p), "hipHostFree");
+  return PLH_OK;
+}
+
+int plh_h2d_async(plh_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (c == nullptr || (bytes > 0 && (dst == nullptr || src == nullptr))) return PLH_ERR_INVALID_ARG;
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  if (bytes == 0) return PLH_OK;
+  PLH_HIP(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(H2D)");
+  return PLH_OK;
+}
+
 int plh_d2h(plh_ctx* c, void* dst, const void* src, size_t bytes) {
   if (c == nullptr || (bytes > 0 && (dst == nullptr || src == nullptr))) return PLH_ERR_INVALID_ARG;
   int rc = use_device(c);

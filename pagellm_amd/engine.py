@@ -108,6 +108,19 @@ class DeviceHistories:
         sp[1::2] = sp[0::2] + np.where(np.asarray(active, dtype=bool), lens, 0)
         return sp
 
+    def spans_and_positions(self, keys: Sequence, active) -> tuple[np.ndarray, np.ndarray]:
+        """spans(keys, active) and append_positions(keys) in one pass."""
+        slots, lens = self._slots_lengths(keys)
+        full = lens >= self.max_len
+        if full.any():
+            key = keys[int(np.argmax(full))]
+            raise RuntimeError(f"history of {key!r} is full ({self.max_len} tokens)")
+        start = slots * self.max_len
+        sp = np.empty(2 * len(keys), dtype=np.int64)
+        sp[0::2] = start
+        sp[1::2] = start + np.where(np.asarray(active, dtype=bool), lens, 0)
+        return sp, start + lens
+
     def append_positions(self, keys: Sequence) -> np.ndarray:
         """int64 [B]: where each row's next id goes."""
         slots, lens = self._slots_lengths(keys)
@@ -180,15 +193,16 @@ class BatchSampler:
             t, k, p, r = _pack_params(params)
             self._packed = (ids, list(params), (t, k, p, r))
         # sampling.py:56: only rows whose penalty is active read their history
-        spans = self.hist.spans(keys, r != 1.0)
-        pos = self.hist.append_positions(keys)
-        # every per-row array in one host buffer, one copy to the device
+        spans, pos = self.hist.spans_and_positions(keys, r != 1.0)
+        # every per-row array in one page-locked host buffer, one queued copy
+        # to the device (the download of the ids below waits for it)
         parts = [t, p, r, u, spans, pos, k]
         offs = np.cumsum([0] + [a.nbytes for a in parts])
-        stage = np.empty(int(offs[-1]), dtype=np.uint8)
+        stage = c.pinned("eng_stage", int(offs[-1]))
         for a, o in zip(parts, offs[:-1]):
             stage[o:o + a.nbytes] = np.ascontiguousarray(a).view(np.uint8)
-        d = c.scratch_upload("eng_stage", stage)
+        d = c.scratch("eng_stage", (int(offs[-1]),), np.uint8)
+        c.h2d_async(d.ptr, stage[:int(offs[-1])])
         d_t, d_p, d_r, d_u, d_sp, d_pos, d_k = (d.ptr + int(o) for o in offs[:-1])
         out = c.scratch("eng_out", (B,), np.int32)
         c.sample(ptr, code, ld, B, V, self.hist.slab.ptr, d_sp, d_t, d_k, d_p, d_r, d_u,

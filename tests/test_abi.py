@@ -76,6 +76,9 @@ def test_null_context_is_an_invalid_argument(lib):
     assert lib.plh_append_ids(None, None, None, None, 1) == -1
     assert lib.plh_copy_rows(None, None, 8, None, 8, 8, 1) == -1
     assert lib.plh_rmsnorm_lm_head(None, None, 4, 1, 4, None, 1e-5, None, 4, 4, None, 4) == -1
+    assert lib.plh_host_alloc(None, None, 8) == -1
+    assert lib.plh_host_free(None, None) == -1
+    assert lib.plh_h2d_async(None, None, None, 8) == -1
     assert lib.plh_last_error(None) == b"null context"
     lib.plh_destroy(None)
 
