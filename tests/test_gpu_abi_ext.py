@@ -110,3 +110,25 @@ def test_quantized_logits_general_path():
             gt, gd = sample_boundary_gaps(x[b], params[b], u[b], ())
             assert gt < 1e-12 or gd < 1e-6, (b, int(ids[b]), ref)
     c.close()
+
+
+def test_pinned_staging_and_queued_copy():
+    """plh_host_alloc / plh_h2d_async: bytes staged in page-locked memory
+    arrive intact once the stream has passed the copy (the next download),
+    at an offset inside a larger device buffer, and a grown staging buffer
+    keeps working."""
+    c = _native.Context(0)
+    try:
+        g = np.random.default_rng(3)
+        for n in (16, 5000, 70000):
+            src = g.integers(0, 256, n, dtype=np.uint8)
+            stage = c.pinned("t", n)
+            stage[:n] = src
+            dev = c.empty((n + 64,), np.uint8)
+            c.h2d_async(dev.ptr + 64, stage[:n])
+            got = np.empty(n, dtype=np.uint8)
+            c._check(c.lib.plh_d2h(c.handle, got.ctypes.data, dev.ptr + 64, n))
+            assert np.array_equal(got, src), n
+            dev.free()
+    finally:
+        c.close()
