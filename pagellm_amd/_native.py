@@ -249,6 +249,25 @@ class Context:
         passed it (the next download or sync)."""
         self._check(self.lib.plh_h2d_async(self.handle, dst_ptr, src.ctypes.data, src.nbytes))
 
+    def stage_upload(self, name: str, parts) -> list[int]:
+        """Copy the host arrays in parts to one device buffer with a single
+        queued copy from a page-locked host buffer, and return each array's
+        device address (16-byte aligned).  Both buffers are reused by the
+        next call with the same name, which the caller makes only after a
+        download or sync has passed this copy."""
+        arrs = [np.ascontiguousarray(a) for a in parts]
+        offs, n = [], 0
+        for a in arrs:
+            offs.append(n)
+            n += (a.nbytes + 15) & ~15
+        d = self.scratch(name, (max(n, 16),), np.uint8)
+        if n:
+            stage = self.pinned(name, n)
+            for a, o in zip(arrs, offs):
+                stage[o:o + a.nbytes] = a.reshape(-1).view(np.uint8)
+            self.h2d_async(d.ptr, stage[:n])
+        return [d.ptr + o for o in offs]
+
     def sync(self) -> None:
         self._check(self.lib.plh_sync(self.handle))
 

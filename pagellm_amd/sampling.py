@@ -181,21 +181,14 @@ def sample_batch(
     u = np.asarray(uniforms, dtype=np.float64).reshape(B) if uniforms is not None else _draw_uniforms(params, rngs, B)
     t, k, p, r = _pack_params(params)
     hist_ids, hist_off = _pack_histories(contexts, params, B, V)
-    d_t = c.scratch_upload("temperature", t)
-    d_k = c.scratch_upload("top_k", k)
-    d_p = c.scratch_upload("top_p", p)
-    d_r = c.scratch_upload("rep_penalty", r)
-    d_u = c.scratch_upload("uniforms", u)
-    d_ids = d_off = None
-    if hist_off is not None:
-        d_ids = c.scratch_upload("hist_ids", hist_ids)
-        d_off = c.scratch_upload("hist_off", hist_off)
+    # the per-row arrays go over in one queued copy, on the stream the
+    # kernels run on (the download below waits for both)
+    parts = [t, p, r, u, k] + ([hist_off, hist_ids] if hist_off is not None else [])
+    d = c.stage_upload("sample_in", parts)
+    d_off, d_ids = (d[5], d[6]) if hist_off is not None else (None, None)
     out = c.scratch("out_ids", (B,), np.int32)
     c.sample(
-        ptr, code, ld, B, V,
-        d_ids.ptr if d_ids is not None else None,
-        d_off.ptr if d_off is not None else None,
-        d_t.ptr, d_k.ptr, d_p.ptr, d_r.ptr, d_u.ptr, out.ptr, None,
+        ptr, code, ld, B, V, d_ids, d_off, d[0], d[4], d[1], d[2], d[3], out.ptr, None,
         _native.PLH_SAMPLE_ROWWISE if rowwise else 0,
     )
     del keep

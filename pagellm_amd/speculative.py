@@ -22,7 +22,7 @@ from __future__ import annotations
 import numpy as np
 
 from . import _native
-from .sampling import _as_float_rows, _expand_params, _pack_histories, _pack_params
+from .sampling import _as_float_rows, _expand_params, _history_ids, _pack_histories, _pack_params
 
 __all__ = ["draft_buffer", "draft_step", "verify", "verify_batch", "verify_step"]
 
@@ -116,29 +116,44 @@ def verify_batch(p, q, draft, accept_u, resample_u, *, ctx: _native.Context | No
     return toks.astype(np.int64), n.astype(np.int64)
 
 
-def _probs_rows(c, x: np.ndarray, params, contexts, uniforms, tag: str):
+def _probs_rows(c, x: np.ndarray, dev, hist, tag: str):
     """plh_sample over the rows of x [N, V] with the processed distributions
-    exported: returns (ids int32 [N] on the host, probs float64 [N, V] on the
+    exported.  dev: device addresses of the per-row (t, k, p, r, u) arrays;
+    hist: (ids, offsets, flags) device addresses of the histories, or None.
+    Returns (ids int32 [N] on the device, probs float64 [N, V] on the
     device)."""
     N, V = x.shape
-    t, k, p, r = _pack_params(params)
-    hist_ids, hist_off = _pack_histories(contexts, params, N, V)
     d_x = c.scratch_upload(f"{tag}_x", x)
-    d_t = c.scratch_upload(f"{tag}_t", t)
-    d_k = c.scratch_upload(f"{tag}_k", k)
-    d_p = c.scratch_upload(f"{tag}_p", p)
-    d_r = c.scratch_upload(f"{tag}_r", r)
-    d_u = c.scratch_upload(f"{tag}_u", np.ascontiguousarray(uniforms, dtype=np.float64))
-    d_ids = d_off = None
-    if hist_off is not None:
-        d_ids = c.scratch_upload(f"{tag}_hid", hist_ids)
-        d_off = c.scratch_upload(f"{tag}_hoff", hist_off)
     out = c.scratch(f"{tag}_out", (N,), np.int32)
     probs = c.scratch(f"{tag}_probs", (N, V), np.float64)
-    c.sample(d_x.ptr, _native.dtype_code(x.dtype), V, N, V, d_ids.ptr if d_ids is not None else None,
-             d_off.ptr if d_off is not None else None, d_t.ptr, d_k.ptr, d_p.ptr, d_r.ptr, d_u.ptr, out.ptr,
-             probs.ptr, 0)
-    return out.download(), probs
+    h_ids, h_off, flags = hist if hist is not None else (None, None, 0)
+    c.sample(d_x.ptr, _native.dtype_code(x.dtype), V, N, V, h_ids, h_off, *dev, out.ptr, probs.ptr, flags)
+    return out, probs
+
+
+def _round_histories(contexts, params, d: np.ndarray, V: int):
+    """The histories of one round's B * (k+1) target rows
+    (``ctx + drafts[:i]``, ``speculative.py:127``) as spans into one id
+    buffer that holds each sequence's context followed by its k drafts once:
+    row (b, i) spans the context and the first i drafts.  Sequences whose
+    penalty is off get empty spans.  Returns (ids int32, spans int64
+    [2 * B * (k+1)]) or (None, None) when no row reads a history."""
+    B, k = d.shape
+    k1 = k + 1
+    parts, spans = [], np.zeros((B, k1, 2), dtype=np.int64)
+    start = 0
+    for b in range(B):
+        if params[b].repetition_penalty == 1.0:
+            continue
+        ctx = contexts[b]
+        ids = _history_ids(ctx if ctx is not None else (), V)
+        parts += [ids, d[b]]
+        spans[b, :, 0] = start
+        spans[b, :, 1] = start + ids.size + np.arange(k1)
+        start += ids.size + k
+    if not parts or start == 0:
+        return None, None
+    return np.concatenate(parts).astype(np.int32, copy=False), spans.reshape(-1)
 
 
 def draft_buffer(B: int, k: int, V: int, *, ctx: _native.Context | None = None):
@@ -166,9 +181,14 @@ def draft_step(logits, params, rngs, contexts, q_out, pos: int, *, ctx: _native.
         raise ValueError(f"q_out {q_out.shape} does not hold position {pos} of a [{B}, k, {V}] round")
     params = _expand_params(params, B)
     u = np.array([rngs[b].random() for b in range(B)], dtype=np.float64)
-    ids, q = _probs_rows(c, x, params, contexts, u, "dft")
+    t, kk, p, r = _pack_params(params)
+    hist_ids, hist_off = _pack_histories(contexts, params, B, V)
+    parts = [t, kk, p, r, u] + ([hist_ids, hist_off] if hist_off is not None else [])
+    d = c.stage_upload("dft_in", parts)
+    hist = (d[5], d[6], 0) if hist_off is not None else None
+    ids, q = _probs_rows(c, x, d[:5], hist, "dft")
     c.copy_rows(q_out.ptr + 8 * pos * V, 8 * k * V, q.ptr, 8 * V, 8 * V, B)
-    return ids.astype(np.int64)
+    return ids.download().astype(np.int64)
 
 
 def verify_step(target_logits, q_rows, drafts, params, rngs, contexts, *, ctx: _native.Context | None = None):
@@ -190,9 +210,10 @@ def verify_step(target_logits, q_rows, drafts, params, rngs, contexts, *, ctx: _
     k = k1 - 1
     d = _check_draft(np.asarray(drafts).reshape(B, k), V)
     params = _expand_params(params, B)
-    rows_params = [params[b] for b in range(B) for _ in range(k1)]
-    rows_ctx = [list(contexts[b]) + [int(t) for t in d[b, :i]] for b in range(B) for i in range(k1)]
-    _, p = _probs_rows(c, x.reshape(B * k1, V), rows_params, rows_ctx, np.zeros(B * k1), "tgt")
+    if contexts is None:
+        contexts = [()] * B
+    if len(contexts) != B:
+        raise ValueError(f"expected {B} contexts, got {len(contexts)}")
     # the draft distributions, [B, k, V] float64 on the device
     qd = None
     if k:
@@ -202,24 +223,30 @@ def verify_step(target_logits, q_rows, drafts, params, rngs, contexts, *, ctx: _
             qd = q_rows
         else:
             qd = c.scratch_upload("tgt_q", np.ascontiguousarray(np.asarray(q_rows, dtype=np.float64).reshape(B, k, V)))
-    # per row: snapshot the Generator, draw k+1 uniforms, replay what was used
+    # per row: snapshot the Generator, draw k+1 uniforms (one call draws the
+    # same values as k+1 calls of random()), replay what was used
     states = [rngs[b].bit_generator.state for b in range(B)]
-    u = np.array([[rngs[b].random() for _ in range(k1)] for b in range(B)], dtype=np.float64)
-    accept_u = np.ascontiguousarray(u[:, :k])
-    draw_u = np.ascontiguousarray(np.stack([u[:, min(s + 1, k)] for s in range(k1)], axis=1))
-    d_d = c.scratch_upload("tgt_d", d) if k else None
-    d_a = c.scratch_upload("tgt_a", accept_u) if k else None
-    d_w = c.scratch_upload("tgt_w", draw_u)
+    u = np.stack([rngs[b].random(k1) for b in range(B)]) if B else np.zeros((0, k1))
+    accept_u = u[:, :k]
+    draw_u = u[:, np.minimum(np.arange(k1) + 1, k)]
+    # the target rows (b, i) share sequence b's parameters; their histories
+    # are spans over each sequence's context and drafts
+    t, kk, p, r = (np.repeat(a, k1) for a in _pack_params(params))
+    hist_ids, spans = _round_histories(contexts, params, d, V)
+    parts = [t, kk, p, r, np.zeros(B * k1), d, accept_u, draw_u]
+    parts += [hist_ids, spans] if spans is not None else []
+    dv = c.stage_upload("tgt_in", parts)
+    hist = (dv[8], dv[9], _native.PLH_SAMPLE_HIST_SPANS) if spans is not None else None
+    _, pr = _probs_rows(c, x.reshape(B * k1, V), dv[:5], hist, "tgt")
     d_tok = c.scratch("tgt_tok", (B, k1), np.int32)
     d_n = c.scratch("tgt_n", (B,), np.int32)
-    c.verify(p.ptr, qd.ptr if k else None, _native.PLH_F64, B, k, V, d_d.ptr if k else None,
-             d_a.ptr if k else None, d_w.ptr, True, d_tok.ptr, d_n.ptr)
+    c.verify(pr.ptr, qd.ptr if k else None, _native.PLH_F64, B, k, V, dv[5] if k else None,
+             dv[6] if k else None, dv[7], True, d_tok.ptr, d_n.ptr)
     toks, n = d_tok.download(), d_n.download()
     emitted = []
     for b in range(B):
         s = int(n[b])
         rngs[b].bit_generator.state = states[b]
-        for _ in range(s + 2 if s < k else k + 1):
-            rngs[b].random()
+        rngs[b].random(s + 2 if s < k else k + 1)
         emitted.append([int(t) for t in toks[b, : s + 1]])
     return emitted, n.astype(np.int64)

@@ -89,3 +89,34 @@ def test_algorithmic_bytes_counts_penalised_histories_only():
 def test_mixed_workload_bytes_formula():
     # 256 x 128256 fp32 + 64 penalised rows x 2048 ids + 48 B/row
     assert 256 * 128256 * 4 + 64 * 2048 * 4 + 256 * 48 == 131870720
+
+
+def test_round_histories_spans_cover_context_and_draft_prefix():
+    """Target row (b, i) of a speculative round reads ``ctx_b + drafts_b[:i]``
+    (speculative.py:127); sequences with the penalty off read nothing."""
+    from pagellm_amd.speculative import _round_histories
+
+    V = 50
+    ctxs = [[1, 2, -1], [7, 8], [], [3]]
+    params = [SamplingParams(repetition_penalty=1.2), SamplingParams(repetition_penalty=1.0),
+              SamplingParams(repetition_penalty=1.1), SamplingParams(repetition_penalty=0.9)]
+    d = np.array([[4, 5], [6, 9], [10, 11], [12, 13]], dtype=np.int32)
+    ids, spans = _round_histories(ctxs, params, d, V)
+    spans = spans.reshape(4, 3, 2)
+    for b in range(4):
+        for i in range(3):
+            got = list(ids[spans[b, i, 0]:spans[b, i, 1]])
+            want = [] if params[b].repetition_penalty == 1.0 else \
+                [t % V for t in ctxs[b]] + list(d[b, :i])
+            assert got == want, (b, i, got, want)
+    # nothing to read at all
+    assert _round_histories([[], []], [SamplingParams()] * 2, np.zeros((2, 0), np.int32), V) == (None, None)
+
+
+def test_bulk_uniform_draws_match_scalar_draws():
+    """Drawing n uniforms in one call consumes the Generator exactly as n
+    calls of ``random()`` do (the speculative round replays this way)."""
+    a, b = make_rng(11, 2), make_rng(11, 2)
+    x = [a.random() for _ in range(6)]
+    assert np.array_equal(np.array(x), b.random(6))
+    assert a.bit_generator.state == b.bit_generator.state
