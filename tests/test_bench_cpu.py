@@ -64,3 +64,18 @@ def test_algorithmic_bytes_of_the_headline_workload():
     B, V = w["logits"].shape
     pen_ids = sum(len(c) for c, p in zip(w["contexts"], w["params"]) if p.repetition_penalty != 1.0)
     assert workloads.algorithmic_bytes(w) == 4 * B * V + 4 * pen_ids + 48 * B == 131_870_720
+
+
+def test_cpu_baseline_reports_one_core_and_all_cores():
+    """The CPU baseline child (no GPU) times the oracle on one pinned core and
+    over a pool of single-core processes, and both agree on the ids."""
+    import json
+    import subprocess
+    import sys
+
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--cpu-baseline-child", "--workload", "char65",
+                        "--cpu-rows", "16", "--cpu-reps", "1"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert out["cores"] == 1 and out["kind"] == "port" and out["value"] > 0
+    assert out["all_cores"]["cores"] >= 1 and out["all_cores"]["value"] > 0
