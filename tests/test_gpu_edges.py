@@ -97,3 +97,44 @@ def test_large_history_duplicates():
     u = np.array([0.0, 0.42])
     ids = sample_batch(x, params, uniforms=u, contexts=ctx)
     _check(x, params, u, ctx, ids)
+
+
+def _shaped_logits(g, kind, B, V):
+    if kind == 0:
+        return g.normal(0, 3, (B, V))
+    if kind == 1:
+        return g.normal(0, 30, (B, V))  # peaky: a handful of tokens hold the mass
+    if kind == 2:
+        return g.normal(0, 0.05, (B, V))  # nearly flat: nuclei of most of the vocabulary
+    if kind == 3:
+        return np.round(g.normal(0, 2, (B, V)) * 4) / 4  # a few hundred distinct values
+    if kind == 4:  # Zipf over a random token order
+        return -np.log(1 + g.permuted(np.tile(np.arange(V), (B, 1)), axis=1)) + g.normal(0, 0.3, (B, V))
+    x = g.normal(0, 2, (B, V))
+    x[:, g.integers(0, V, max(1, V // 3))] = -np.inf  # a third of the vocabulary masked
+    return x
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_random_batches_across_shapes(seed):
+    """Random batches over vocabularies from 3 to 152064 (chunk edges
+    included), six logit shapes, both input precisions, mixed per-row
+    parameters (greedy, extreme temperatures, top-k above V, tiny and
+    near-one top_p, penalties on both sides of 1) and histories with
+    negative ids and duplicates, against the oracle row by row."""
+    for it in range(12):
+        g = np.random.default_rng(seed * 1000 + it)
+        V = int(g.choice([3, 100, 4097, 16383, 16384, 16385, 32000, 50257, 128256, 152064]))
+        B = int(g.integers(1, 40))
+        kind = int(g.integers(0, 6))
+        dtype = np.float64 if g.random() < 0.25 else np.float32
+        x = _shaped_logits(g, kind, B, V).astype(dtype)
+        params = [SamplingParams(temperature=float(g.choice([0.0, 1.0, 0.6, 1.5, 1e-3, 5.0])),
+                                 top_k=int(g.choice([0, 0, 1, 7, 40, 400, 600, 5000, V, V + 1])),
+                                 top_p=float(g.choice([1.0, 1.0, 0.9, 0.95, 0.99, 0.5, 1e-6, 0.999999])),
+                                 repetition_penalty=float(g.choice([1.0, 1.0, 1.1, 1.3, 0.8, 2.0])))
+                  for _ in range(B)]
+        H = int(g.choice([0, 10, 500, 2048, 6000]))
+        ctx = [list(g.integers(-V, V, int(g.integers(0, H + 1)))) for _ in range(B)]
+        u = g.random(B)
+        _check(x, params, u, ctx, sample_batch(x, params, uniforms=u, contexts=ctx))

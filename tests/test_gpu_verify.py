@@ -171,3 +171,45 @@ def test_verify_draw_ends_of_the_cdf():
             rt, rn = oracle.verify_batch(pp, q, np.array([[V - 1]]), np.array([[0.999]]), np.array([u]))
             assert n[0] == rn[0] == 0
             assert toks[0][0] == rt[0][0] == (lo if u == 0.0 else hi - 1), (lo, hi, u, toks, rt)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_random_verify_batches(seed):
+    """Random batches: k from 0 to 6, V from 2 to 70000 (chunk edges
+    included), smooth, peaky and one-hot distributions, identical draft and
+    target rows, drafts at the argmax or anywhere q is positive, in float64
+    and float32.  float32 inputs are widened exactly and processed in
+    float64, so they are compared with the oracle on the same values as
+    float64 arrays."""
+    for it in range(10):
+        g = np.random.default_rng(77 + seed * 1000 + it)
+        B, k = int(g.integers(1, 40)), int(g.integers(0, 7))
+        V = int(g.choice([2, 50, 4096, 4097, 32000, 70000]))
+
+        def dist(shape):
+            m = int(g.integers(0, 3))
+            if m == 2:  # one-hot rows (greedy drafts and targets)
+                z = np.full(shape, -np.inf)
+                np.put_along_axis(z, g.integers(0, V, shape[:-1])[..., None], 0.0, -1)
+            else:
+                z = g.normal(0, [2.0, 20.0][m], shape)
+            e = np.exp(z - z.max(-1, keepdims=True))
+            return e / e.sum(-1, keepdims=True)
+
+        p, q = dist((B, k + 1, V)), dist((B, k, V))
+        if k and g.random() < 0.3:
+            q = p[:, :k].copy()
+        draft = np.zeros((B, k), dtype=np.int64)
+        for b in range(B):
+            for i in range(k):
+                t = int(np.argmax(q[b, i])) if g.random() < 0.5 else int(g.integers(0, V))
+                draft[b, i] = t if q[b, i, t] > 0 else int(np.argmax(q[b, i]))
+        au, ru = g.random((B, k)), g.random(B)
+        if g.random() < 0.5:
+            p, q = p.astype(np.float32), q.astype(np.float32)
+        toks, n = verify_batch(p, q, draft, au, ru)
+        p64, q64 = p.astype(np.float64), q.astype(np.float64)
+        rt, rn = oracle.verify_batch(p64, q64, draft, au, ru)
+        for b in np.nonzero((n != rn) | (toks != rt).any(1))[0]:
+            gap = verify_boundary_gap(p64[b], q64[b], list(draft[b]), au[b], float(ru[b]))
+            assert gap < 1e-6, (it, int(b), toks[b].tolist(), rt[b].tolist(), gap)
