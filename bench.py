@@ -511,6 +511,15 @@ def main() -> None:
     kernel_ms = stream_ms / max(1, calls)
     merge_avg_ms = merge_ms / max(1, calls)
 
+    # each step bracketed on its own, for the spread across steps
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for i, (e0, e1) in enumerate(evs):
+        e0.record(stream)
+        step(i)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    per_step = np.array([e0.elapsed_time(e1) for e0, e1 in evs])
+
     ids = out.cpu().numpy()
     greedy = [i for i, pp in enumerate(w["params"]) if pp.greedy]
     if greedy and not np.array_equal(ids[greedy], np.argmax(w["logits"][greedy], axis=1)):
@@ -550,6 +559,8 @@ def main() -> None:
         "data": "synthetic",
         "config": {"workload": args.workload, "batch": B, "vocab": V, "logits_dtype": "fp32",
                    "rotating_input_sets": args.sets, "algorithmic_bytes_per_step": algo_bytes},
+        "step_ms_spread": {"median": float(np.median(per_step)), "p10": float(np.percentile(per_step, 10)),
+                           "p90": float(np.percentile(per_step, 90)), "max": float(per_step.max())},
         "step_hbm_gbps": gbps,
         "step_hbm_frac": gbps / PEAK_HBM_GBPS,
         "kernel_ms": {"k_sample_chunks": kernel_ms, "k_sample_final": merge_avg_ms},
