@@ -152,7 +152,7 @@ def pmc_probe(workload: str) -> None:
     import torch
 
     from pagellm_amd import _native, workloads
-    from pagellm_amd.sampling import _pack_histories, _pack_params
+    from pagellm_amd.sampling import _nucleus_hint, _pack_histories, _pack_params
 
     w = workloads.WORKLOADS[workload]()
     B, V = w["logits"].shape
@@ -160,6 +160,7 @@ def pmc_probe(workload: str) -> None:
     ctx = _native.Context(0)
     ctx.set_stream(torch.cuda.current_stream().cuda_stream)
     t, k, p, r = _pack_params(w["params"])
+    hint = _nucleus_hint(t, k, p, w["logits"].shape[1])
     hist_ids, hist_off = _pack_histories(w["contexts"], w["params"], B, V)
     x = torch.from_numpy(w["logits"]).to(dev)
     d = {n: torch.from_numpy(a).to(dev) for n, a in
@@ -173,7 +174,7 @@ def pmc_probe(workload: str) -> None:
         ctx.sample(x.data_ptr(), _native.PLH_F32, V, B, V,
                    d["ids"].data_ptr() if "ids" in d else None, d["off"].data_ptr() if "off" in d else None,
                    d["t"].data_ptr(), d["k"].data_ptr(), d["p"].data_ptr(), d["r"].data_ptr(),
-                   d["u"].data_ptr(), out.data_ptr(), None, 0)
+                   d["u"].data_ptr(), out.data_ptr(), None, hint)
     torch.cuda.synchronize()
     ctx.close()
     print("pmc probe done", flush=True)
@@ -223,7 +224,7 @@ def bench_config(name: str, steps: int = 20, warmup: int = 3) -> dict:
     import torch
 
     from pagellm_amd import _native, workloads
-    from pagellm_amd.sampling import _pack_histories, _pack_params
+    from pagellm_amd.sampling import _nucleus_hint, _pack_histories, _pack_params
 
     w = workloads.WORKLOADS[name]()
     B, V = w["logits"].shape
@@ -232,6 +233,7 @@ def bench_config(name: str, steps: int = 20, warmup: int = 3) -> dict:
     ctx = _native.Context(0)
     ctx.set_stream(stream.cuda_stream)
     t, k, p, r = _pack_params(w["params"])
+    hint = _nucleus_hint(t, k, p, w["logits"].shape[1])
     hist_ids, hist_off = _pack_histories(w["contexts"], w["params"], B, V)
     xs = [torch.from_numpy(w["logits"]).to(dev) for _ in range(2)]
     d = {n: torch.from_numpy(a).to(dev) for n, a in
@@ -243,7 +245,7 @@ def bench_config(name: str, steps: int = 20, warmup: int = 3) -> dict:
         ctx.sample(xs[i % 2].data_ptr(), _native.PLH_F32, V, B, V,
                    d["ids"].data_ptr() if "ids" in d else None, d["off"].data_ptr() if "off" in d else None,
                    d["t"].data_ptr(), d["k"].data_ptr(), d["p"].data_ptr(), d["r"].data_ptr(),
-                   d["u"].data_ptr(), out.data_ptr(), None, 0)
+                   d["u"].data_ptr(), out.data_ptr(), None, hint)
 
     fb0 = ctx.fallback_rows()
     with torch.cuda.stream(stream):
@@ -460,7 +462,7 @@ def main() -> None:
     import torch
 
     from pagellm_amd import _native, workloads
-    from pagellm_amd.sampling import _pack_histories, _pack_params
+    from pagellm_amd.sampling import _nucleus_hint, _pack_histories, _pack_params
 
     print(f"[bench] generating {args.workload}", file=sys.stderr, flush=True)
     w = workloads.WORKLOADS[args.workload]()
@@ -474,6 +476,7 @@ def main() -> None:
     torch.cuda.set_stream(stream)
 
     t, k, p, r = _pack_params(w["params"])
+    hint = _nucleus_hint(t, k, p, w["logits"].shape[1])
     hist_ids, hist_off = _pack_histories(w["contexts"], w["params"], B, V)
     logits = [torch.from_numpy(w["logits"]).to(dev) for _ in range(args.sets)]
     d = {n: torch.from_numpy(a).to(dev) for n, a in
@@ -486,7 +489,7 @@ def main() -> None:
         ctx.sample(x.data_ptr(), _native.PLH_F32, V, B, V,
                    d["ids"].data_ptr() if "ids" in d else None, d["off"].data_ptr() if "off" in d else None,
                    d["t"].data_ptr(), d["k"].data_ptr(), d["p"].data_ptr(), d["r"].data_ptr(),
-                   d["u"].data_ptr(), out.data_ptr(), None, 0)
+                   d["u"].data_ptr(), out.data_ptr(), None, hint)
 
     fb0 = ctx.fallback_rows()
     for i in range(args.warmup):

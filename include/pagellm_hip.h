@@ -47,6 +47,11 @@ extern "C" {
                                    hist_ids instead of B+1 CSR offsets, so
                                    histories can live in fixed per-sequence
                                    slots that grow in place (plh_append_ids) */
+#define PLH_SAMPLE_NUCLEUS 4 /* performance hint, same results: rows with no
+                                top-k and top_p >= 0.98 (nuclei that hold most
+                                of the vocabulary) take a three-pass path over
+                                all chunks instead of the per-row general
+                                pipeline; costs three extra launches */
 
 /* plh_set_option options */
 #define PLH_OPT_KERNEL_TIMING 1 /* value 1: bracket the fast path's kernels with

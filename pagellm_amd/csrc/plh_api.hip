@@ -308,6 +308,7 @@ int plh_sample(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, int
   a.out_ids = out_ids;
   a.out_probs = out_probs;
   a.fallback_rows = c->fallback;
+  a.nucleus = (flags & PLH_SAMPLE_NUCLEUS) ? 1 : 0;
   const bool f64 = dtype == PLH_F64;
   // the fast path gathers per-row state in LDS sized for V <= 262144
   if (out_probs != nullptr || (flags & PLH_SAMPLE_ROWWISE) || V > kMaxVBitmap) {

@@ -17,8 +17,26 @@ struct WavePart {
   int end;        // candidate rows: end of the wave's slots in its chunk's list
                   // (the chunk's candidate count is the largest end)
   int flags;      // kChunkIncomplete: the row needs the general pipeline
+  double zmin;    // nucleus rows: smallest finite penalised logit (+inf if none)
 };
 constexpr int kChunkIncomplete = 1;
+
+// Per-row state of the nucleus path (rows with no top-k and a top_p of at
+// least kNucTopP, when the caller asks for it): three passes over the row
+// (segment partials, a count histogram of y = z / T, the tokens of the
+// bins that can hold the cut) instead of the general pipeline.
+struct NucRow {
+  double ymax;   // largest y of the row
+  double S;      // sum over the row of exp(y - ymax)
+  double invS;
+  double ylo;    // lower edge of the histogram (the smallest finite y)
+  double scale;  // bins per unit of y
+  int state;     // kNucActive while the nucleus kernels own the row
+  int general;   // 1: too few distinct values; k_nuc_final runs the general pipeline
+  int dlo, dhi;  // bins [dlo, dhi] hold the candidates (written by the second pass)
+};
+constexpr int kNucActive = 1;
+constexpr int kNucBins = 2048;
 
 // Workspace of the two-launch fast path, carved from one device buffer.
 struct ChunkWs {
@@ -27,6 +45,10 @@ struct ChunkWs {
   double* seg_s;    // [B * C * 8] per-wave segment sum of exp(z / T - max)
   double* cz;       // [B * C * capc] candidate penalised logits
   int32_t* ci;      // [B * C * capc] candidate token ids
+  NucRow* nrow;     // [B] nucleus path: per-row state
+  uint32_t* ncnt;   // [B * kNucBins] nucleus path: token counts per y bin
+  double* nexcl;    // [B * C * 8] nucleus path: per-segment mass below the candidate bins
+  int32_t* ncand;   // [B * C] nucleus path: candidates per chunk (-1: over capacity)
   int C;            // chunks per row
   int capc;         // candidate slots per chunk
 };
@@ -46,6 +68,7 @@ struct SampleArgs {
   int32_t* out_ids;
   double* out_probs;
   unsigned long long* fallback_rows;  // rows finished by the general path
+  int nucleus;                        // 1: eligible rows take the nucleus path
   ChunkWs ws;                         // fast path only
 };
 

@@ -48,6 +48,7 @@ struct RowParams {
   int top_k;
   int64_t h0, h1;  // history ids [h0, h1) of the CSR arrays
   bool greedy, pen_active, topk, topp;
+  bool nucleus;  // the row takes the nucleus path of the fast kernels
 };
 
 // sampling.py:59-61: divide positive logits, multiply the others.

@@ -28,7 +28,7 @@ from typing import Hashable, Sequence
 import numpy as np
 
 from . import _native
-from .sampling import _draw_uniforms, _expand_params, _history_ids, _is_torch_cuda, _pack_params
+from .sampling import _draw_uniforms, _expand_params, _history_ids, _is_torch_cuda, _nucleus_hint, _pack_params
 
 __all__ = ["BatchSampler", "DeviceHistories"]
 
@@ -206,7 +206,7 @@ class BatchSampler:
         d_t, d_p, d_r, d_u, d_sp, d_pos, d_k = (d.ptr + int(o) for o in offs[:-1])
         out = c.scratch("eng_out", (B,), np.int32)
         c.sample(ptr, code, ld, B, V, self.hist.slab.ptr, d_sp, d_t, d_k, d_p, d_r, d_u,
-                 out.ptr, None, _native.PLH_SAMPLE_HIST_SPANS)
+                 out.ptr, None, _native.PLH_SAMPLE_HIST_SPANS | _nucleus_hint(t, k, p, V))
         # llm_engine.py:284: the token joins the history, on the device
         c.append_ids(self.hist.slab.ptr, d_pos, out.ptr, B)
         ids = out.download().astype(np.int64)

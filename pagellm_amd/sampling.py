@@ -116,6 +116,18 @@ def _expand_params(params, B: int) -> list[SamplingParams]:
     return params
 
 
+NUCLEUS_TOP_P = 0.98  # rows with no top-k from this top_p up may take the nucleus path
+
+
+def _nucleus_hint(t: np.ndarray, k: np.ndarray, p: np.ndarray, V: int) -> int:
+    """``PLH_SAMPLE_NUCLEUS`` when some row is non-greedy with no top-k and
+    ``NUCLEUS_TOP_P <= top_p < 1``: such nuclei hold most of the vocabulary,
+    which the three-pass path handles faster than the per-row general
+    pipeline.  The sampled ids do not depend on the hint."""
+    rows = (t != 0) & ((k <= 0) | (k >= V)) & (p >= NUCLEUS_TOP_P) & (p < 1.0)
+    return _native.PLH_SAMPLE_NUCLEUS if bool(rows.any()) else 0
+
+
 def _draw_uniforms(params, rngs, B: int) -> np.ndarray:
     """One ``rng.random()`` per non-greedy row, in row order."""
     u = np.zeros(B, dtype=np.float64)
@@ -189,7 +201,7 @@ def sample_batch(
     out = c.scratch("out_ids", (B,), np.int32)
     c.sample(
         ptr, code, ld, B, V, d_ids, d_off, d[0], d[4], d[1], d[2], d[3], out.ptr, None,
-        _native.PLH_SAMPLE_ROWWISE if rowwise else 0,
+        _native.PLH_SAMPLE_ROWWISE if rowwise else _nucleus_hint(t, k, p, V),
     )
     del keep
     return out.download().astype(np.int64)

@@ -213,7 +213,7 @@ def test_general_path_inside_fast_kernel():
     V = 50000
     x = g.normal(0, 0.05, (4, V)).astype(np.float32)
     params = [SamplingParams(top_p=0.9), SamplingParams(top_k=30000), SamplingParams(top_k=30000, top_p=0.5),
-              SamplingParams(top_p=0.999, temperature=2.0)]
+              SamplingParams(top_p=0.97, temperature=2.0)]
     u = g.random(4)
     c = _native.default_context()
     before = c.fallback_rows()
@@ -234,3 +234,68 @@ def test_penalize_matches_reference_rule():
         ref = oracle.apply_repetition_penalty(x, ctx, 1.7)
         assert got.dtype == ref.dtype == dt
         assert np.array_equal(got, ref)
+
+
+def _nucleus_batch(g, V, B, kind, dtype):
+    if kind == "zipf":
+        x = -np.log(1 + g.permuted(np.tile(np.arange(V), (B, 1)), axis=1)) + g.normal(0, 0.3, (B, V))
+    elif kind == "flat":
+        x = g.normal(0, 0.05, (B, V))
+    elif kind == "masked":
+        x = g.normal(0, 2, (B, V))
+        x[:, g.integers(0, V, V // 2)] = -np.inf
+    elif kind == "ties":
+        x = np.round(g.normal(0, 1, (B, V)) * 2) / 2
+    else:
+        x = g.normal(0, 3, (B, V))
+    return x.astype(dtype)
+
+
+@pytest.mark.parametrize("kind", ["zipf", "flat", "masked", "ties", "normal"])
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_nucleus_path_matches_oracle(kind, dtype):
+    """Rows with no top-k and top_p >= 0.98 take the three-pass nucleus path
+    (sample_batch sets the hint): against the oracle and the row-wise
+    kernel, with penalties on both sides of 1, temperatures, vocabularies
+    at and off the chunk size, and rows mixed with other modes."""
+    g = np.random.default_rng(2 * ["zipf", "flat", "masked", "ties", "normal"].index(kind) + (dtype == np.float64))
+    for V in (16384, 50257, 152064):
+        B = 12
+        x = _nucleus_batch(g, V, B, kind, dtype)
+        params = [SamplingParams(top_p=float(g.choice([0.98, 0.99, 0.995, 0.999999])),
+                                 temperature=float(g.choice([1.0, 0.7, 1.6])),
+                                 repetition_penalty=float(g.choice([1.0, 1.05, 0.9])))
+                  for _ in range(B - 2)]
+        params += [SamplingParams(temperature=0.0), SamplingParams(top_k=40, top_p=0.99)]
+        # histories short enough that no chunk sets aside more penalised
+        # tokens than its pools hold (which would send the row to the
+        # general pipeline in every mode)
+        ctx = [list(g.integers(-V, V, int(g.integers(0, min(3000, V // 32))))) for _ in range(B)]
+        u = g.random(B)
+        c = _native.default_context()
+        before = c.fallback_rows()
+        ids = sample_batch(x, params, uniforms=u, contexts=ctx)
+        if kind in ("zipf", "normal"):  # no row needs the general pipeline
+            assert c.fallback_rows() == before, (kind, V)
+        w = dict(logits=x, params=params, contexts=ctx, uniforms=u)
+        _compare_rows(w, range(B), ids, f"nucleus-{kind}-{V}")
+        assert np.array_equal(ids, sample_batch(x, params, uniforms=u, contexts=ctx, rowwise=True))
+
+
+def test_nucleus_path_hands_rows_to_the_general_pipeline():
+    """A row with a single distinct finite value, and a row whose cut window
+    outgrows the candidate slots (a wide flat band at the cut), are finished
+    by the general pipeline inside the nucleus kernels."""
+    V = 40000
+    x = np.zeros((3, V), dtype=np.float32)
+    x[1, : V // 2] = 1.0  # two values: half the vocabulary ties at the cut
+    x[2] = np.random.default_rng(3).normal(0, 1, V)
+    params = [SamplingParams(top_p=0.99)] * 3
+    u = np.array([0.3, 0.6, 0.9])
+    c = _native.default_context()
+    before = c.fallback_rows()
+    ids = sample_batch(x, params, uniforms=u)
+    assert c.fallback_rows() - before == 2
+    w = dict(logits=x, params=params, contexts=[[]] * 3, uniforms=u)
+    _compare_rows(w, range(3), ids, "nucleus-general")
+    assert np.array_equal(ids, sample_batch(x, params, uniforms=u, rowwise=True))
