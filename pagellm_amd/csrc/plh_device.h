@@ -28,6 +28,7 @@ constexpr int kWaves = kThreads / kWave;
 
 // 2^62: probabilities (each <= 1, sum ~1) become exact-addable integers.
 constexpr double kFxScale = 4611686018427387904.0;
+constexpr uint64_t kFxOne = 1ull << 62;  // kFxScale as an integer: probability 1
 
 __device__ __forceinline__ int lane() { return threadIdx.x & (kWave - 1); }
 

@@ -26,14 +26,14 @@ constexpr int kChunkIncomplete = 1;
 // (segment partials, a count histogram of y = z / T, the tokens of the
 // bins that can hold the cut) instead of the general pipeline.
 struct NucRow {
-  double ymax;   // largest y of the row
+  double zlo;    // lower edge of the count histogram: the smallest finite penalised logit
+  double scale;  // bins per unit of z
+  double ymax;   // largest y = z / T of the row
   double S;      // sum over the row of exp(y - ymax)
   double invS;
-  double ylo;    // lower edge of the histogram (the smallest finite y)
-  double scale;  // bins per unit of y
   int state;     // kNucActive while the nucleus kernels own the row
-  int general;   // 1: too few distinct values; k_nuc_final runs the general pipeline
-  int dlo, dhi;  // bins [dlo, dhi] hold the candidates (written by the second pass)
+  int general;   // 1: k_nuc_final runs the general pipeline on the row
+  int dlo, dhi;  // bins [dlo, dhi] hold the candidates
 };
 constexpr int kNucActive = 1;
 constexpr int kNucBins = 2048;

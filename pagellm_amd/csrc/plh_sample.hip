@@ -627,7 +627,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       if (z > -INFINITY) zmn = fmin(zmn, z);
     }
     zmn = wave_min(zmn);
-    if (lane() == 0) wp->zmin = zmn;
+    const double zmx = wave_max(lmax);
+    if (lane() == 0) {
+      wp->zmin = zmn;
+      wp->zmax = zmx;
+    }
   }
   if (!rp.topk) {  // the full-vocabulary normaliser (sampling.py:79-81)
     // y = z / T is monotone in z, so the segment's max y is y(max z)
@@ -1318,7 +1322,26 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   if (!general && rp.nucleus) {  // the nucleus kernels finish the row
     uint32_t* cnt = a.ws.ncnt + (size_t)row * kNucBins;
     for (int b = threadIdx.x; b < kNucBins; b += kThreads) cnt[b] = 0u;
-    if (threadIdx.x == 0) a.ws.nrow[row].state = kNucActive;
+    if (wave() == 0) {
+      // the count histogram spans the row's finite penalised logits
+      const WavePart* pp = a.ws.part + (size_t)row * a.ws.C * kWaves;
+      double lo = INFINITY, hi = -INFINITY;
+      for (int j = lane(); j < a.ws.C * kWaves; j += kWave) {
+        lo = fmin(lo, pp[j].zmin);
+        hi = fmax(hi, pp[j].zmax);
+      }
+      lo = wave_min(lo);
+      hi = wave_max(hi);
+      if (lane() == 0) {
+        const double scale = (double)kNucBins / (hi - lo);
+        NucRow& nr = a.ws.nrow[row];
+        nr.zlo = lo;
+        nr.scale = scale;
+        // one distinct finite value, or none: the general pipeline
+        nr.general = (hi - lo > 0.0 && hi - lo < INFINITY && scale < INFINITY) ? 0 : 1;
+        nr.state = kNucActive;
+      }
+    }
     return;
   }
   if (general) {
@@ -1344,123 +1367,25 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
 // ================================================================ nucleus
 // Rows with no top-k and top_p >= kNucTopP keep most of the vocabulary
 // (top_p 0.99 over a Zipf-like distribution keeps ~90% of it), more than
-// any candidate list holds.  With the caller's hint they take three passes
-// over all chunks instead of one workgroup per row: k_sample_chunks leaves
-// the segment partials of the normaliser (and each wave's smallest finite
-// logit), k_sample_final sets up the row, then
-//   k_nuc_hist   counts the row's tokens in kNucBins affine bins of y = z/T;
-//   k_nuc_cands  bounds each bin's mass by its count and the exp of its
-//                edges, which brackets the top-p cut (sampling.py:82-90) in a
-//                window of bins: the bins below it hold at most 1 - top_p
-//                of the mass (dropped), those above it more than that below
-//                them (kept).  The window's tokens become candidates; the
-//                mass of the tokens below it is summed per segment;
-//   k_nuc_final  finds the cut among the candidates in (p desc, idx asc)
-//                order, starting from the mass above the window, then draws
-//                (sampling.py:94-98): the segment where the kept mass
-//                crosses u * total, rescanned from HBM.
-// Every workgroup of a row derives the same window from the same counts in
-// the same order.  A row whose window does not fit its candidate slots, or
-// whose cut falls outside the window, is finished by the general pipeline.
-
-struct NucWin {
-  int dlo, dhi;  // candidate bins [dlo, dhi]; dhi == INT_MAX: no window
-  uint64_t n;    // tokens in the window
-};
-
-// The window from the row's counts (k_nuc_cands, every workgroup of the
-// row).  Bin b spans y in [ylo + b / scale, ylo + (b + 1) / scale) up to
-// rounding; 0.01 of a bin of margin on each edge, the bottom bin open below
-// and the top one closed at ymax.  U(b) = mass bound of bins below b from
-// their upper edges, L(b + 1) = mass bound of bins up to b from their lower
-// edges.  dlo = the largest b with U(b) <= (1 - top_p) S; dhi = the smallest
-// b with L(b + 1) > (1 - top_p) S.
-__device__ __forceinline__ NucWin nuc_window(const uint32_t* gcnt, const NucRow& nr, double top_p, const double* tab,
-                                             ChunkSmem& cm) {
-  constexpr int kPer = kNucBins / kThreads;
-  const int b0 = kPer * (int)threadIdx.x;
-  uint32_t c[kPer];
-  double lo[kPer], hi[kPer], slo = 0.0, shi = 0.0;
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int b = b0 + j;
-    c[j] = gcnt[b];
-    const double y0 = b == 0 ? -INFINITY : nr.ylo + ((double)b - 0.01) / nr.scale;
-    const double y1 = b == kNucBins - 1 ? nr.ymax : nr.ylo + ((double)b + 1.01) / nr.scale;
-    lo[j] = c[j] ? (double)c[j] * fast_exp_neg(fmin(y0 - nr.ymax, 0.0), tab) * (1.0 - 1e-12) : 0.0;
-    hi[j] = c[j] ? (double)c[j] * fast_exp_neg(fmin(y1 - nr.ymax, 0.0), tab) * (1.0 + 1e-12) : 0.0;
-    slo += lo[j];
-    shi += hi[j];
-  }
-  const double ilo = wave_scan_incl(slo, 0.0, OpAdd{}), ihi = wave_scan_incl(shi, 0.0, OpAdd{});
-  if (lane() == kWave - 1) {
-    cm.redd[wave()] = ilo;
-    cm.redd[kWaves + wave()] = ihi;
-  }
-  wg_barrier();
-  double l = wave_shift_up1(ilo, 0.0), u = wave_shift_up1(ihi, 0.0);
-  for (int w = 0; w < wave(); ++w) {
-    l += cm.redd[w];
-    u += cm.redd[kWaves + w];
-  }
-  const double thr = (1.0 - top_p) * nr.S;
-  int mlo = -1, mhi = INT_MAX;
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    if (u <= thr) mlo = b0 + j;
-    l += lo[j];
-    if (mhi == INT_MAX && l > thr) mhi = b0 + j;
-    u += hi[j];
-  }
-  mlo = wave_max(mlo);
-  mhi = wave_min(mhi);
-  if (lane() == 0) {
-    cm.ctl[wave()] = mlo;
-    cm.redi[wave()] = mhi;
-  }
-  wg_barrier();
-  NucWin r{-1, INT_MAX, 0};
-  for (int w = 0; w < kWaves; ++w) {
-    r.dlo = max(r.dlo, cm.ctl[w]);
-    r.dhi = min(r.dhi, cm.redi[w]);
-  }
-  uint64_t n = 0;
-#pragma unroll
-  for (int j = 0; j < kPer; ++j)
-    if (b0 + j >= r.dlo && b0 + j <= r.dhi) n += c[j];
-  n = wave_sum(n);
-  if (lane() == 0) cm.redu[wave()] = n;
-  wg_barrier();
-  r.n = 0;
-  for (int w = 0; w < kWaves; ++w) r.n += cm.redu[w];
-  return r;
-}
-
-// A nucleus row's normaliser from the segment partials and its range of y
-// = z / T, the bins of its count histogram (each wave of k_nuc_hist derives
-// the same from the first pass's parts).  false: fewer than two distinct
-// finite values; the general pipeline finishes the row.
-template <typename TIn>
-__device__ __forceinline__ bool nuc_row_setup(const SampleArgs& a, int row, const RowParams& rp, const double* tab,
-                                              NucRow& nr) {
-  SegLoad sg;
-  load_segs(a, row, (a.V + Geo<TIn>::kSeg - 1) / Geo<TIn>::kSeg, sg);
-  const int P = a.ws.C * kWaves;
-  const WavePart* pp = a.ws.part + (size_t)row * P;
-  double zm = INFINITY;
-  for (int j = lane(); j < P; j += kWave) zm = fmin(zm, pp[j].zmin);
-  zm = uniform(wave_min(zm));
-  double ms[kSegPerLane], lex;
-  const SegNorm sn = seg_norm(sg, tab, ms, &lex);
-  const YScale ys{rp.T, 1.0 / rp.T};
-  nr.ymax = sn.ymax;
-  nr.S = sn.S;
-  nr.invS = 1.0 / sn.S;
-  nr.ylo = ys(zm);
-  const double span = sn.ymax - nr.ylo;
-  nr.scale = (double)kNucBins / span;
-  return span > 0.0 && span < INFINITY && nr.scale < INFINITY;
-}
+// any candidate list holds.  With the caller's hint they take passes over
+// all chunks instead of one workgroup per row: k_sample_chunks leaves the
+// segment partials of the normaliser and each wave's smallest and largest
+// finite logit, k_sample_final spreads kNucBins affine bins over the row's
+// range of z, then
+//   k_nuc_hist    counts the row's tokens per bin;
+//   k_nuc_window  bounds each bin's mass by its count and the exp of its
+//                 edges, which brackets the top-p cut (sampling.py:82-90) in a
+//                 window of bins: the bins below it hold at most 1 - top_p
+//                 of the mass (dropped), those above it more than that below
+//                 them (kept);
+//   k_nuc_cands   writes the window's tokens as candidates and sums the mass
+//                 below the window per segment;
+//   k_nuc_final   finds the cut among the candidates in (p desc, idx asc)
+//                 order, starting from the mass above the window, then draws
+//                 (sampling.py:94-98): the segment where the kept mass
+//                 crosses u * total, rescanned from HBM.
+// A row whose window does not fit its candidate slots, or whose cut falls
+// outside the window, is finished by the general pipeline.
 
 // p of a nucleus row's token: exp(y - ymax) / S.
 __device__ __forceinline__ double nuc_p(double y, const NucRow& nr, const double* tab) {
@@ -1477,24 +1402,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const int row = g / C;
   const RowParams rp = load_row_params(a, row);
   if (!rp.nucleus) return;
-  if (a.ws.nrow[row].state != kNucActive) return;
+  const NucRow nr = a.ws.nrow[row];
+  if (nr.state != kNucActive || nr.general != 0) return;
   const int c0 = (g - row * C) * G::kChunk;
   const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
   ChunkToks<TIn> tk;
   load_chunk<TIn, VEC>(x, a.V, c0, tk.v);
-  init_exp_table_wave(cm.exp_tab[wave()]);
-  NucRow nr;
-  const bool ok = nuc_row_setup<TIn>(a, row, rp, cm.exp_tab[wave()], nr);
-  if (g == row * C && threadIdx.x == 0) {  // for the next two kernels
-    NucRow& w = a.ws.nrow[row];
-    w.ymax = nr.ymax;
-    w.S = nr.S;
-    w.invS = nr.invS;
-    w.ylo = nr.ylo;
-    w.scale = nr.scale;
-    w.general = ok ? 0 : 1;
-  }
-  if (!ok) return;
   for (int b = threadIdx.x; b < kNucBins; b += kThreads) nh[b] = 0u;
   if (rp.pen_active) {
     // the first pass set aside the same tokens without overflow, or the
@@ -1503,17 +1416,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     set_aside_penalised<TIn>(tk, pb, rp.pen, c0, cm);
   }
   wg_barrier();
-  const YScale ys{rp.T, 1.0 / rp.T};
-  const Affine af{nr.ylo, nr.scale, kNucBins};
+  const Affine af{nr.zlo, nr.scale, kNucBins};
   tk.new_pass();
 #pragma unroll
   for (int e = 0; e < G::kEpt; ++e) {
     const TIn v = tk.rv(e);
-    if (v > (TIn)(-INFINITY)) lds_add(&nh[af.bin(ys((double)v))], 1u);
+    if (v > (TIn)(-INFINITY)) lds_add(&nh[af.bin((double)v)], 1u);
   }
   for (int i = 0; i < tk.np; ++i) {
     const double z = tk.pen_z(cm, i);
-    if (z > -INFINITY) lds_add(&nh[af.bin(ys(z))], 1u);
+    if (z > -INFINITY) lds_add(&nh[af.bin(z)], 1u);
   }
   wg_barrier();
   uint32_t* cnt = a.ws.ncnt + (size_t)row * kNucBins;
@@ -1523,11 +1435,109 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   }
 }
 
+struct NucWinSmem {
+  double exp_tab[kWaves][64];
+  double redd[2 * kWaves];
+  int redi[2 * kWaves];
+  uint64_t redu[kWaves];
+};
+
+// One workgroup per nucleus row: the normaliser from the segment partials
+// and the window of candidate bins.  Bin b spans z in [zlo + b / scale,
+// zlo + (b + 1) / scale) up to rounding: 0.01 of a bin of margin on each
+// edge, the bottom bin open below and the top one closed at ymax.  U(b) =
+// mass bound of the bins below b from their upper edges, L(b + 1) = mass
+// bound of the bins up to b from their lower edges; dlo = the largest b with
+// U(b) <= (1 - top_p) S, dhi = the smallest b with L(b + 1) > (1 - top_p) S.
+template <typename TIn>
+__global__ __launch_bounds__(kThreads) void k_nuc_window(SampleArgs a) {
+  using G = Geo<TIn>;
+  __shared__ NucWinSmem sm;
+  const int row = blockIdx.x;
+  const RowParams rp = load_row_params(a, row);
+  if (!rp.nucleus) return;
+  const NucRow nr = a.ws.nrow[row];
+  if (nr.state != kNucActive || nr.general != 0) return;
+  init_exp_table_wave(sm.exp_tab[wave()]);
+  const double* tab = sm.exp_tab[wave()];
+  constexpr int kPer = kNucBins / kThreads;
+  const int b0 = kPer * (int)threadIdx.x;
+  uint32_t c[kPer];
+  const uint32_t* gcnt = a.ws.ncnt + (size_t)row * kNucBins;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) c[j] = gcnt[b0 + j];
+  SegLoad sg;
+  load_segs(a, row, (a.V + G::kSeg - 1) / G::kSeg, sg);
+  double ms[kSegPerLane], lex;
+  const SegNorm sn = seg_norm(sg, tab, ms, &lex);
+  const double invT = 1.0 / rp.T;
+  double lo[kPer], hi[kPer], slo = 0.0, shi = 0.0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int b = b0 + j;
+    const double y0 = b == 0 ? -INFINITY : (nr.zlo + ((double)b - 0.01) / nr.scale) * invT;
+    const double y1 = b == kNucBins - 1 ? sn.ymax : (nr.zlo + ((double)b + 1.01) / nr.scale) * invT;
+    lo[j] = c[j] ? (double)c[j] * fast_exp_neg(fmin(y0 - sn.ymax, 0.0), tab) * (1.0 - 1e-12) : 0.0;
+    hi[j] = c[j] ? (double)c[j] * fast_exp_neg(fmin(y1 - sn.ymax, 0.0), tab) * (1.0 + 1e-12) : 0.0;
+    slo += lo[j];
+    shi += hi[j];
+  }
+  const double ilo = wave_scan_incl(slo, 0.0, OpAdd{}), ihi = wave_scan_incl(shi, 0.0, OpAdd{});
+  if (lane() == kWave - 1) {
+    sm.redd[wave()] = ilo;
+    sm.redd[kWaves + wave()] = ihi;
+  }
+  wg_barrier();
+  double l = wave_shift_up1(ilo, 0.0), u = wave_shift_up1(ihi, 0.0);
+  for (int w = 0; w < wave(); ++w) {
+    l += sm.redd[w];
+    u += sm.redd[kWaves + w];
+  }
+  const double thr = (1.0 - rp.top_p) * sn.S;
+  int mlo = -1, mhi = INT_MAX;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    if (u <= thr) mlo = b0 + j;
+    l += lo[j];
+    if (mhi == INT_MAX && l > thr) mhi = b0 + j;
+    u += hi[j];
+  }
+  mlo = wave_max(mlo);
+  mhi = wave_min(mhi);
+  if (lane() == 0) {
+    sm.redi[wave()] = mlo;
+    sm.redi[kWaves + wave()] = mhi;
+  }
+  wg_barrier();
+  int dlo = -1, dhi = INT_MAX;
+  for (int w = 0; w < kWaves; ++w) {
+    dlo = max(dlo, sm.redi[w]);
+    dhi = min(dhi, sm.redi[kWaves + w]);
+  }
+  uint64_t n = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j)
+    if (b0 + j >= dlo && b0 + j <= dhi) n += c[j];
+  n = wave_sum(n);
+  if (lane() == 0) sm.redu[wave()] = n;
+  wg_barrier();
+  if (threadIdx.x == 0) {
+    uint64_t tot = 0;
+    for (int w = 0; w < kWaves; ++w) tot += sm.redu[w];
+    NucRow& out = a.ws.nrow[row];
+    out.ymax = sn.ymax;
+    out.S = sn.S;
+    out.invS = 1.0 / sn.S;
+    out.dlo = dlo;
+    out.dhi = dhi;
+    out.general = (dhi == INT_MAX || dhi < dlo || tot > (uint64_t)a.ws.C * a.ws.capc) ? 1 : 0;
+  }
+}
+
 template <typename TIn, bool VEC>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_nuc_cands(SampleArgs a) {
   using G = Geo<TIn>;
   __shared__ ChunkSmem cm;
-  __shared__ int over;
   const int C = a.ws.C;
   const int capc = a.ws.capc;
   const int g = blockIdx.x;
@@ -1539,87 +1549,51 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const int c0 = (g - row * C) * G::kChunk;
   const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
   ChunkToks<TIn> tk;
-  load_chunk<TIn, VEC>(x, a.V, c0, tk.v);  // in flight while the window is found
-  const double* tab = cm.exp_tab[wave()];
+  load_chunk<TIn, VEC>(x, a.V, c0, tk.v);
   init_exp_table_wave(cm.exp_tab[wave()]);
-  if (threadIdx.x == 0) {  // ordered before use by the window's barriers
-    cm.cand_n = 0;
-    over = 0;
-  }
-  const NucWin win = nuc_window(a.ws.ncnt + (size_t)row * kNucBins, nr, rp.top_p, tab, cm);
-  if (g == row * C && threadIdx.x == 0) {
-    a.ws.nrow[row].dlo = win.dlo;
-    a.ws.nrow[row].dhi = win.dhi;
-  }
-  if (win.dhi == INT_MAX || win.dhi < win.dlo || win.n > (uint64_t)C * capc) {
-    if (threadIdx.x == 0) a.ws.ncand[g] = -1;
-    return;
-  }
+  const double* tab = cm.exp_tab[wave()];
+  if (threadIdx.x == 0) cm.cand_n = 0;
   if (rp.pen_active) {
     const uint32_t pb = chunk_pbits<TIn>(a, rp, c0, cm);
     set_aside_penalised<TIn>(tk, pb, rp.pen, c0, cm);
   }
+  wg_barrier();
   const YScale ys{rp.T, 1.0 / rp.T};
-  const Affine af{nr.ylo, nr.scale, kNucBins};
-  // mass below the window; tokens in it
+  const Affine af{nr.zlo, nr.scale, kNucBins};
+  double* cz = a.ws.cz + (size_t)g * capc;
+  int32_t* ci = a.ws.ci + (size_t)g * capc;
+  // the mass below the window, and the window's tokens (slot order does not
+  // matter: the last kernel orders them by key and index)
   double ex = 0.0;
-  int cnt = 0;
   tk.new_pass();
 #pragma unroll
   for (int e = 0; e < G::kEpt; ++e) {
     const TIn v = tk.rv(e);
     if (v > (TIn)(-INFINITY)) {
-      const double y = ys((double)v);
-      const int b = af.bin(y);
-      if (b < win.dlo) ex += nuc_p(y, nr, tab);
-      else if (b <= win.dhi) ++cnt;
+      const double z = (double)v;
+      const int b = af.bin(z);
+      if (b < nr.dlo) {
+        ex += nuc_p(ys(z), nr, tab);
+      } else if (b <= nr.dhi) {
+        const int slot = lds_fetch_add(&cm.cand_n, 1);
+        if (slot < capc) {
+          cz[slot] = nuc_p(ys(z), nr, tab);
+          ci[slot] = c0 + slot_q<TIn>(e);
+        }
+      }
     }
   }
   for (int i = 0; i < tk.np; ++i) {
     const double z = tk.pen_z(cm, i);
     if (z > -INFINITY) {
-      const double y = ys(z);
-      const int b = af.bin(y);
-      if (b < win.dlo) ex += nuc_p(y, nr, tab);
-      else if (b <= win.dhi) ++cnt;
-    }
-  }
-  // one LDS reservation per wave; the wave writes its candidates (p and
-  // token id) to its range of the chunk's slots
-  const int incl = wave_scan_incl(cnt, 0, OpAdd{});
-  const int wtot = lane_value(incl, kWave - 1);
-  int base = 0;
-  if (lane() == kWave - 1 && wtot > 0) base = lds_fetch_add(&cm.cand_n, wtot);
-  base = lane_value(base, kWave - 1);
-  if (base + wtot > capc) {
-    if (lane() == 0) over = 1;
-  } else if (cnt > 0) {
-    int slot = base + incl - cnt;
-    double* cz = a.ws.cz + (size_t)g * capc;
-    int32_t* ci = a.ws.ci + (size_t)g * capc;
-    tk.new_pass();
-#pragma unroll
-    for (int e = 0; e < G::kEpt; ++e) {
-      const TIn v = tk.rv(e);
-      if (v > (TIn)(-INFINITY)) {
-        const double y = ys((double)v);
-        const int b = af.bin(y);
-        if (b >= win.dlo && b <= win.dhi) {
-          cz[slot] = nuc_p(y, nr, tab);
-          ci[slot] = c0 + slot_q<TIn>(e);
-          ++slot;
-        }
-      }
-    }
-    for (int i = 0; i < tk.np; ++i) {
-      const double z = tk.pen_z(cm, i);
-      if (z > -INFINITY) {
-        const double y = ys(z);
-        const int b = af.bin(y);
-        if (b >= win.dlo && b <= win.dhi) {
-          cz[slot] = nuc_p(y, nr, tab);
+      const int b = af.bin(z);
+      if (b < nr.dlo) {
+        ex += nuc_p(ys(z), nr, tab);
+      } else if (b <= nr.dhi) {
+        const int slot = lds_fetch_add(&cm.cand_n, 1);
+        if (slot < capc) {
+          cz[slot] = nuc_p(ys(z), nr, tab);
           ci[slot] = tk.pen_tok(cm, i);
-          ++slot;
         }
       }
     }
@@ -1627,7 +1601,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   ex = wave_sum(ex);
   if (lane() == 0) a.ws.nexcl[(size_t)g * kWaves + wave()] = ex;
   wg_barrier();
-  if (threadIdx.x == 0) a.ws.ncand[g] = over ? -1 : cm.cand_n;
+  if (threadIdx.x == 0) a.ws.ncand[g] = cm.cand_n > capc ? -1 : cm.cand_n;
 }
 
 template <typename TIn, bool VEC>
@@ -1659,143 +1633,151 @@ __global__ __launch_bounds__(kThreads) void k_nuc_final(SampleArgs a) {
   const int csh = __ffs(capc) - 1;
   const int slots = C * capc;
   const int nseg = C * kWaves;
-  // every candidate slot into registers; the chunks' counts per wave
-  RegCands rc;
-  gather_cands(a, row, rc);
-  int* wc = fs.wcnt[wave()];
-  int bad = 0;
-  for (int c = lane(); c < C; c += kWave) {
-    const int n = a.ws.ncand[(size_t)row * C + c];
-    bad |= n < 0 ? 1 : 0;
-    wc[c] = n < 0 ? 0 : n;
-  }
-  bool general = nr.general != 0 || uniform(wave_max(bad)) != 0;
+  bool general = nr.general != 0;
   int id = V - 1;
   if (!general) {
-    rc.valid = 0;
-    uint32_t pos = 0;
-    double cs = 0.0;
-#pragma unroll
-    for (int q = 0; q < kPerT; ++q) {
-      const int i = q * kThreads + (int)threadIdx.x;
-      rc.w[q] = 0ull;
-      if (i < slots && (i & (capc - 1)) < wc[i >> csh]) {
-        rc.valid |= 1u << q;
-        if (rc.v[q] > 0.0) pos |= 1u << q;
-        rc.w[q] = to_fx(rc.v[q]);
-        cs += rc.v[q];
-      }
+    // every candidate slot into registers; the chunks' counts per wave
+    RegCands rc;
+    gather_cands(a, row, rc);
+    int* wc = fs.wcnt[wave()];
+    int bad = 0;
+    for (int c = lane(); c < C; c += kWave) {
+      const int n = a.ws.ncand[(size_t)row * C + c];
+      bad |= n < 0 ? 1 : 0;
+      wc[c] = n < 0 ? 0 : n;
     }
-    const double cp = xw_sum(xw, cs);
-    double dl = 0.0;
-    for (int s = lane(); s < nseg; s += kWave) dl += a.ws.nexcl[(size_t)row * nseg + s];
-    const double dp = uniform(wave_sum(dl));
-    // the mass above the window, then the cut among the candidates
-    const uint64_t above = to_fx(1.0 - dp - cp);
-    const uint64_t target = topp_target(rp.top_p);
-    SelOut r{false, true, 0, 0};
-    if (above < target)
-      r = select_desc<true>(pos, rc, [](double p) { return pkey_of(p); }, target - above, V, fs.rl[1], fs, xw, hgen);
-    if (!r.found || r.giveup) {
-      general = true;
-    } else {
-      // candidates past the cut, by segment (fixed point)
-      Hist& h = next_hist(fs, hgen);
+    general = uniform(wave_max(bad)) != 0;
+    if (!general) {
+      rc.valid = 0;
+      uint32_t pos = 0;
+      uint64_t ws = 0;
 #pragma unroll
       for (int q = 0; q < kPerT; ++q) {
-        if (((rc.valid >> q) & 1u) && rc.w[q] != 0ull) {
-          const uint64_t k = pkey_of(rc.v[q]);
-          if (!(k > r.key || (k == r.key && rc.idx[q] <= r.idx))) lds_add(&h.mass[rc.idx[q] / G::kSeg], rc.w[q]);
+        const int i = q * kThreads + (int)threadIdx.x;
+        rc.w[q] = 0ull;
+        if (i < slots && (i & (capc - 1)) < wc[i >> csh]) {
+          rc.valid |= 1u << q;
+          if (rc.v[q] > 0.0) pos |= 1u << q;
+          rc.w[q] = to_fx(rc.v[q]);
+          ws += rc.w[q];
         }
       }
-      wg_barrier();
-      // kept mass per segment: its share of the normaliser less what lies
-      // below the window and the candidates past the cut
-      const int nsv = (V + G::kSeg - 1) / G::kSeg;
-      SegLoad sg;
-      load_segs(a, row, nsv, sg);
-      double ms[kSegPerLane], lex;
-      seg_norm(sg, tab, ms, &lex);
-      double kk[kSegPerLane], ks = 0.0;
+      // the window's fixed-point mass (exact, in any slot order) and the
+      // mass below it (segment sums in a fixed order)
+      const auto sw = xw.post(wave_sum(ws), 0, 0);
+      uint64_t wsum = 0;
 #pragma unroll
-      for (int j = 0; j < kSegPerLane; ++j) {
-        const int s = kSegPerLane * lane() + j;
-        kk[j] = 0.0;
-        if (s < nsv) {
-          kk[j] = ms[j] * nr.invS - a.ws.nexcl[(size_t)row * nseg + s] - (double)h.mass[s] * (1.0 / kFxScale);
-          if (!(kk[j] > 0.0)) kk[j] = 0.0;
-        }
-        ks += kk[j];
-      }
-      const double kin = wave_scan_incl(ks, 0.0, OpAdd{});
-      const double t = rp.u * uniform(lane_value(kin, kWave - 1));
-      double run = kin - ks, bl = 0.0;
-      int kl = INT_MAX;
-#pragma unroll
-      for (int j = 0; j < kSegPerLane; ++j) {
-        if (kl == INT_MAX && kk[j] > 0.0 && run + kk[j] > t) {
-          kl = kSegPerLane * lane() + j;
-          bl = run;
-        }
-        run += kk[j];
-      }
-      const uint64_t hits = __ballot(kl != INT_MAX);
-      if (hits == 0) {
+      for (int w = 0; w < kWaves; ++w) wsum += sw[0][w];
+      double dl = 0.0;
+      for (int s = lane(); s < nseg; s += kWave) dl += a.ws.nexcl[(size_t)row * nseg + s];
+      const uint64_t below_and_in = to_fx(uniform(wave_sum(dl))) + wsum;
+      const uint64_t total = kFxOne;
+      const uint64_t above = below_and_in < total ? total - below_and_in : 0ull;
+      const uint64_t target = topp_target(rp.top_p);
+      SelOut r{false, true, 0, 0};
+      if (above < target)
+        r = select_desc<true>(pos, rc, [](double p) { return pkey_of(p); }, target - above, V, fs.rl[1], fs, xw,
+                              hgen);
+      if (!r.found || r.giveup) {
         general = true;
       } else {
-        const int L = __builtin_ctzll(hits);
-        const int kstar = uniform(lane_value(kl, L));
-        const double before = uniform(lane_value(bl, L));
-        const int s0 = kstar * G::kSeg;
-        if (rp.pen_active) {
-          for (int w = threadIdx.x; w < G::kSeg / 32; w += kThreads) fs.segbits[w] = 0u;
-          wg_barrier();
-          for (int64_t hh = rp.h0 + threadIdx.x; hh < rp.h1; hh += kThreads) {
-            const int off = a.hist_ids[hh] - s0;
-            if ((unsigned)off < (unsigned)G::kSeg) lds_or(&fs.segbits[off >> 5], 1u << (off & 31));
-          }
-          wg_barrier();
-        }
-        // thread t holds tokens s0 + kPer*t + q, in vocabulary order
-        constexpr int kPer = G::kSeg / kThreads;
-        const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
-        const YScale ys{rp.T, 1.0 / rp.T};
-        const Affine af{nr.ylo, nr.scale, kNucBins};
-        const int q0 = kPer * (int)threadIdx.x;
-        double e[kPer], es = 0.0;
+        // candidates past the cut, by segment (fixed point)
+        Hist& h = next_hist(fs, hgen);
 #pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-          e[q] = 0.0;
-          const int p = s0 + q0 + q;
-          if (p < V) {
-            double z = (double)x[p];
-            if (rp.pen_active && ((fs.segbits[(q0 + q) >> 5] >> ((q0 + q) & 31)) & 1u)) z = penalize(z, rp.pen);
-            if (z > -INFINITY) {
-              const double y = ys(z);
-              const int b = af.bin(y);
-              if (b >= nr.dlo) {
-                const double pz = nuc_p(y, nr, tab);
-                const uint64_t k = pkey_of(pz);
-                if (b > nr.dhi || k > r.key || (k == r.key && p <= r.idx)) e[q] = pz;
+        for (int q = 0; q < kPerT; ++q) {
+          if (((rc.valid >> q) & 1u) && rc.w[q] != 0ull) {
+            const uint64_t k = pkey_of(rc.v[q]);
+            if (!(k > r.key || (k == r.key && rc.idx[q] <= r.idx))) lds_add(&h.mass[rc.idx[q] / G::kSeg], rc.w[q]);
+          }
+        }
+        wg_barrier();
+        // kept mass per segment: its share of the normaliser less what lies
+        // below the window and the candidates past the cut
+        const int nsv = (V + G::kSeg - 1) / G::kSeg;
+        SegLoad sg;
+        load_segs(a, row, nsv, sg);
+        double ms[kSegPerLane], lex;
+        seg_norm(sg, tab, ms, &lex);
+        double kk[kSegPerLane], ks = 0.0;
+#pragma unroll
+        for (int j = 0; j < kSegPerLane; ++j) {
+          const int s = kSegPerLane * lane() + j;
+          kk[j] = 0.0;
+          if (s < nsv) {
+            kk[j] = ms[j] * nr.invS - a.ws.nexcl[(size_t)row * nseg + s] - (double)h.mass[s] * (1.0 / kFxScale);
+            if (!(kk[j] > 0.0)) kk[j] = 0.0;
+          }
+          ks += kk[j];
+        }
+        const double kin = wave_scan_incl(ks, 0.0, OpAdd{});
+        const double t = rp.u * uniform(lane_value(kin, kWave - 1));
+        double run = kin - ks, bl = 0.0;
+        int kl = INT_MAX;
+#pragma unroll
+        for (int j = 0; j < kSegPerLane; ++j) {
+          if (kl == INT_MAX && kk[j] > 0.0 && run + kk[j] > t) {
+            kl = kSegPerLane * lane() + j;
+            bl = run;
+          }
+          run += kk[j];
+        }
+        const uint64_t hits = __ballot(kl != INT_MAX);
+        if (hits == 0) {
+          general = true;
+        } else {
+          const int L = __builtin_ctzll(hits);
+          const int kstar = uniform(lane_value(kl, L));
+          const double before = uniform(lane_value(bl, L));
+          const int s0 = kstar * G::kSeg;
+          if (rp.pen_active) {
+            for (int w = threadIdx.x; w < G::kSeg / 32; w += kThreads) fs.segbits[w] = 0u;
+            wg_barrier();
+            for (int64_t hh = rp.h0 + threadIdx.x; hh < rp.h1; hh += kThreads) {
+              const int off = a.hist_ids[hh] - s0;
+              if ((unsigned)off < (unsigned)G::kSeg) lds_or(&fs.segbits[off >> 5], 1u << (off & 31));
+            }
+            wg_barrier();
+          }
+          // thread t holds tokens s0 + kPer*t + q, in vocabulary order
+          constexpr int kPer = G::kSeg / kThreads;
+          const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
+          const YScale ys{rp.T, 1.0 / rp.T};
+          const Affine af{nr.zlo, nr.scale, kNucBins};
+          const int q0 = kPer * (int)threadIdx.x;
+          double e[kPer], es = 0.0;
+#pragma unroll
+          for (int q = 0; q < kPer; ++q) {
+            e[q] = 0.0;
+            const int p = s0 + q0 + q;
+            if (p < V) {
+              double z = (double)x[p];
+              if (rp.pen_active && ((fs.segbits[(q0 + q) >> 5] >> ((q0 + q) & 31)) & 1u)) z = penalize(z, rp.pen);
+              if (z > -INFINITY) {
+                const int b = af.bin(z);
+                if (b >= nr.dlo) {
+                  const double pz = nuc_p(ys(z), nr, tab);
+                  const uint64_t k = pkey_of(pz);
+                  if (b > nr.dhi || k > r.key || (k == r.key && p <= r.idx)) e[q] = pz;
+                }
               }
             }
+            es += e[q];
           }
-          es += e[q];
-        }
-        double pex, ptot;
-        xw_scan(xw, es, &pex, &ptot);
-        double rr = pex;
-        int hit = INT_MAX, last = -1;
+          double pex, ptot;
+          xw_scan(xw, es, &pex, &ptot);
+          double rr = pex;
+          int hit = INT_MAX, last = -1;
 #pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-          rr += e[q];
-          if (e[q] > 0.0) last = s0 + q0 + q;
-          if (hit == INT_MAX && e[q] > 0.0 && before + rr > t) hit = s0 + q0 + q;
+          for (int q = 0; q < kPer; ++q) {
+            rr += e[q];
+            if (e[q] > 0.0) last = s0 + q0 + q;
+            if (hit == INT_MAX && e[q] > 0.0 && before + rr > t) hit = s0 + q0 + q;
+          }
+          hit = xw_min(xw, hit);
+          if (hit == INT_MAX) hit = xw_max(xw, last);  // rounding at the segment end
+          if (hit < 0) general = true;
+          else id = hit;
         }
-        hit = xw_min(xw, hit);
-        if (hit == INT_MAX) hit = xw_max(xw, last);  // rounding at the segment end
-        if (hit < 0) general = true;
-        else id = hit;
       }
     }
   }
@@ -1953,6 +1935,7 @@ hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, int num_c
     auto fin = f64 ? (vec ? k_nuc_final<double, true> : k_nuc_final<double, false>)
                    : (vec ? k_nuc_final<float, true> : k_nuc_final<float, false>);
     hipLaunchKernelGGL(hist, dim3(total), block, 0, s, a);
+    hipLaunchKernelGGL(f64 ? k_nuc_window<double> : k_nuc_window<float>, gf, block, 0, s, a);
     hipLaunchKernelGGL(cands, dim3(total), block, 0, s, a);
     hipLaunchKernelGGL(fin, gf, block, 0, s, a);
   }
