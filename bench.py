@@ -435,7 +435,7 @@ def main() -> None:
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the other workloads (zipf32k, zipf152k, char65, spec32k verify)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
-    ap.add_argument("--only", choices=["spec32k", "head128k"],
+    ap.add_argument("--only", choices=["spec32k", "head128k", "zipf32k", "zipf152k", "char65"],
                     help="run one of the other configurations alone and print its JSON (for profiling)")
     args = ap.parse_args()
 
@@ -449,7 +449,8 @@ def main() -> None:
         pmc_probe(args.workload)
         return
     if args.only:
-        fn = {"spec32k": bench_verify, "head128k": bench_head}[args.only]
+        fns = {"spec32k": bench_verify, "head128k": bench_head}
+        fn = fns.get(args.only, lambda **kw: bench_config(args.only, **kw))
         print(json.dumps(fn(steps=min(args.steps, 50), warmup=min(args.warmup, 5))), flush=True)
         return
     if args.gpus != 1:
