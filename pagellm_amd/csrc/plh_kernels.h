@@ -34,6 +34,7 @@ struct NucRow {
   int state;     // kNucActive while the nucleus kernels own the row
   int general;   // 1: k_nuc_final runs the general pipeline on the row
   int dlo, dhi;  // bins [dlo, dhi] hold the candidates
+  int above;     // 1: nexcl sums the tokens above the window (fewer than those below)
 };
 constexpr int kNucActive = 1;
 constexpr int kNucBins = 2048;
@@ -47,7 +48,7 @@ struct ChunkWs {
   int32_t* ci;      // [B * C * capc] candidate token ids
   NucRow* nrow;     // [B] nucleus path: per-row state
   uint32_t* ncnt;   // [B * kNucBins] nucleus path: token counts per y bin
-  double* nexcl;    // [B * C * 8] nucleus path: per-segment mass below the candidate bins
+  double* nexcl;    // [B * C * 8] nucleus path: per-segment mass on one side of the candidate bins
   int32_t* ncand;   // [B * C] nucleus path: candidates per chunk (-1: over capacity)
   int C;            // chunks per row
   int capc;         // candidate slots per chunk

@@ -1387,6 +1387,18 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
 // A row whose window does not fit its candidate slots, or whose cut falls
 // outside the window, is finished by the general pipeline.
 
+// Bin of a nucleus row's token: floor((z - zlo) * scale) clamped to
+// [0, kNucBins - 1], computed in float32 on z rounded to float.  Monotone
+// non-decreasing in z; every kernel that bins a token uses this function.
+struct NucBin {
+  float lo, scale;
+  __device__ __forceinline__ explicit NucBin(const NucRow& nr) : lo((float)nr.zlo), scale((float)nr.scale) {}
+  __device__ __forceinline__ int operator()(double z) const {
+    const float t = ((float)z - lo) * scale;
+    return (int)__builtin_amdgcn_fmed3f(t, 0.0f, (float)(kNucBins - 1));
+  }
+};
+
 // p of a nucleus row's token: exp(y - ymax) / S.
 __device__ __forceinline__ double nuc_p(double y, const NucRow& nr, const double* tab) {
   return fast_exp_neg(y - nr.ymax, tab) * nr.invS;
@@ -1416,16 +1428,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     set_aside_penalised<TIn>(tk, pb, rp.pen, c0, cm);
   }
   wg_barrier();
-  const Affine af{nr.zlo, nr.scale, kNucBins};
+  const NucBin nb(nr);
   tk.new_pass();
 #pragma unroll
   for (int e = 0; e < G::kEpt; ++e) {
     const TIn v = tk.rv(e);
-    if (v > (TIn)(-INFINITY)) lds_add(&nh[af.bin((double)v)], 1u);
+    if (v > (TIn)(-INFINITY)) lds_add(&nh[nb((double)v)], 1u);
   }
   for (int i = 0; i < tk.np; ++i) {
     const double z = tk.pen_z(cm, i);
-    if (z > -INFINITY) lds_add(&nh[af.bin(z)], 1u);
+    if (z > -INFINITY) lds_add(&nh[nb(z)], 1u);
   }
   wg_barrier();
   uint32_t* cnt = a.ws.ncnt + (size_t)row * kNucBins;
@@ -1440,12 +1452,14 @@ struct NucWinSmem {
   double redd[2 * kWaves];
   int redi[2 * kWaves];
   uint64_t redu[kWaves];
+  uint64_t redu2[2 * kWaves];
 };
 
 // One workgroup per nucleus row: the normaliser from the segment partials
-// and the window of candidate bins.  Bin b spans z in [zlo + b / scale,
-// zlo + (b + 1) / scale) up to rounding: 0.01 of a bin of margin on each
-// edge, the bottom bin open below and the top one closed at ymax.  U(b) =
+// and the window of candidate bins.  Bin b spans z in [lo + b / scale,
+// lo + (b + 1) / scale) (NucBin's float lo and scale) up to rounding: a
+// margin of 0.01 bin plus the float rounding of z on each edge, the bottom
+// bin open below and the top one closed at ymax.  U(b) =
 // mass bound of the bins below b from their upper edges, L(b + 1) = mass
 // bound of the bins up to b from their lower edges; dlo = the largest b with
 // U(b) <= (1 - top_p) S, dhi = the smallest b with L(b + 1) > (1 - top_p) S.
@@ -1471,12 +1485,19 @@ __global__ __launch_bounds__(kThreads) void k_nuc_window(SampleArgs a) {
   double ms[kSegPerLane], lex;
   const SegNorm sn = seg_norm(sg, tab, ms, &lex);
   const double invT = 1.0 / rp.T;
+  // NucBin works in float32: its edges are those of the rounded lo and
+  // scale, and rounding z to float moves a token by up to 2^-24 |z|, which
+  // the margin covers with room to spare
+  const NucBin nbin(nr);
+  const double flo = (double)nbin.lo, fsc = (double)nbin.scale;
+  const double mag = fmax(fabs(flo), fabs(flo + (double)kNucBins / fsc));
+  const double mb = 0.01 + mag * fsc * 2.5e-7;
   double lo[kPer], hi[kPer], slo = 0.0, shi = 0.0;
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int b = b0 + j;
-    const double y0 = b == 0 ? -INFINITY : (nr.zlo + ((double)b - 0.01) / nr.scale) * invT;
-    const double y1 = b == kNucBins - 1 ? sn.ymax : (nr.zlo + ((double)b + 1.01) / nr.scale) * invT;
+    const double y0 = b == 0 ? -INFINITY : (flo + ((double)b - mb) / fsc) * invT;
+    const double y1 = b == kNucBins - 1 ? sn.ymax : (flo + ((double)b + 1.0 + mb) / fsc) * invT;
     lo[j] = c[j] ? (double)c[j] * fast_exp_neg(fmin(y0 - sn.ymax, 0.0), tab) * (1.0 - 1e-12) : 0.0;
     hi[j] = c[j] ? (double)c[j] * fast_exp_neg(fmin(y1 - sn.ymax, 0.0), tab) * (1.0 + 1e-12) : 0.0;
     slo += lo[j];
@@ -1514,17 +1535,32 @@ __global__ __launch_bounds__(kThreads) void k_nuc_window(SampleArgs a) {
     dlo = max(dlo, sm.redi[w]);
     dhi = min(dhi, sm.redi[kWaves + w]);
   }
-  uint64_t n = 0;
+  uint64_t n = 0, nb = 0, na = 0;
 #pragma unroll
-  for (int j = 0; j < kPer; ++j)
-    if (b0 + j >= dlo && b0 + j <= dhi) n += c[j];
+  for (int j = 0; j < kPer; ++j) {
+    const int b = b0 + j;
+    if (b >= dlo && b <= dhi) n += c[j];
+    else if (b < dlo) nb += c[j];
+    else na += c[j];
+  }
   n = wave_sum(n);
-  if (lane() == 0) sm.redu[wave()] = n;
+  nb = wave_sum(nb);
+  na = wave_sum(na);
+  if (lane() == 0) {
+    sm.redu[wave()] = n;
+    sm.redu2[wave()] = nb;
+    sm.redu2[kWaves + wave()] = na;
+  }
   wg_barrier();
   if (threadIdx.x == 0) {
-    uint64_t tot = 0;
-    for (int w = 0; w < kWaves; ++w) tot += sm.redu[w];
+    uint64_t tot = 0, below = 0, abv = 0;
+    for (int w = 0; w < kWaves; ++w) {
+      tot += sm.redu[w];
+      below += sm.redu2[w];
+      abv += sm.redu2[kWaves + w];
+    }
     NucRow& out = a.ws.nrow[row];
+    out.above = abv < below ? 1 : 0;
     out.ymax = sn.ymax;
     out.S = sn.S;
     out.invS = 1.0 / sn.S;
@@ -1534,10 +1570,20 @@ __global__ __launch_bounds__(kThreads) void k_nuc_window(SampleArgs a) {
   }
 }
 
+constexpr int kNucStage = 256;                   // tokens a wave stages before summing their mass
+constexpr int kNucCandWave = kCapChunk / kWaves;  // window tokens a wave stages
+
+// The window's tokens go to the candidate slots (p and id); the tokens on
+// the row's smaller side of the window (nr.above) have their p summed per
+// segment.  Both are first staged per wave in LDS (a ballot and a bit count
+// per token step), so the exps run densely over the staged tokens instead
+// of in a branch nearly every wave would take.
 template <typename TIn, bool VEC>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_nuc_cands(SampleArgs a) {
   using G = Geo<TIn>;
   __shared__ ChunkSmem cm;
+  __shared__ double stz[kWaves][kNucStage];
+  __shared__ int over;
   const int C = a.ws.C;
   const int capc = a.ws.capc;
   const int g = blockIdx.x;
@@ -1552,56 +1598,73 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   load_chunk<TIn, VEC>(x, a.V, c0, tk.v);
   init_exp_table_wave(cm.exp_tab[wave()]);
   const double* tab = cm.exp_tab[wave()];
-  if (threadIdx.x == 0) cm.cand_n = 0;
+  if (threadIdx.x == 0) {
+    cm.cand_n = 0;
+    over = 0;
+  }
   if (rp.pen_active) {
     const uint32_t pb = chunk_pbits<TIn>(a, rp, c0, cm);
     set_aside_penalised<TIn>(tk, pb, rp.pen, c0, cm);
   }
   wg_barrier();
   const YScale ys{rp.T, 1.0 / rp.T};
-  const Affine af{nr.zlo, nr.scale, kNucBins};
-  double* cz = a.ws.cz + (size_t)g * capc;
-  int32_t* ci = a.ws.ci + (size_t)g * capc;
-  // the mass below the window, and the window's tokens (slot order does not
-  // matter: the last kernel orders them by key and index)
-  double ex = 0.0;
+  const NucBin nb(nr);
+  const bool abv = nr.above != 0;
+  double* sz = stz[wave()];
+  StageRaw* cs = cm.sraw + wave() * kNucCandWave;
+  uint32_t* cc = cm.scode + wave() * kNucCandWave;
+  const uint64_t below_me = (1ull << lane()) - 1ull;
+  double acc = 0.0;  // this lane's share of the side's mass
+  int mn = 0, cn = 0;  // staged side tokens and window tokens (the same in every lane)
+  auto flush = [&]() {
+    for (int i = lane(); i < mn; i += kWave) acc += nuc_p(ys(sz[i]), nr, tab);
+    mn = 0;
+  };
+  auto take = [&](double z, int idx) {
+    const bool fin = z > -INFINITY;
+    const int b = nb(z);
+    const bool side = fin && (abv ? b > nr.dhi : b < nr.dlo);
+    const bool cand = fin && b >= nr.dlo && b <= nr.dhi;
+    const uint64_t ms = __ballot(side);
+    if (ms != 0ull) {
+      if (side) sz[mn + __popcll(ms & below_me)] = z;
+      mn += __popcll(ms);
+      if (mn > kNucStage - kWave) flush();
+    }
+    const uint64_t mc = __ballot(cand);
+    if (mc != 0ull) {
+      const int slot = cn + __popcll(mc & below_me);
+      if (cand && slot < kNucCandWave) {
+        cs[slot].d = z;
+        cc[slot] = (uint32_t)idx;
+      }
+      cn += __popcll(mc);
+    }
+  };
   tk.new_pass();
 #pragma unroll
-  for (int e = 0; e < G::kEpt; ++e) {
-    const TIn v = tk.rv(e);
-    if (v > (TIn)(-INFINITY)) {
-      const double z = (double)v;
-      const int b = af.bin(z);
-      if (b < nr.dlo) {
-        ex += nuc_p(ys(z), nr, tab);
-      } else if (b <= nr.dhi) {
-        const int slot = lds_fetch_add(&cm.cand_n, 1);
-        if (slot < capc) {
-          cz[slot] = nuc_p(ys(z), nr, tab);
-          ci[slot] = c0 + slot_q<TIn>(e);
-        }
-      }
+  for (int e = 0; e < G::kEpt; ++e) take((double)tk.rv(e), c0 + slot_q<TIn>(e));
+  const int npmax = wave_max(tk.np);
+  for (int i = 0; i < npmax; ++i) take(i < tk.np ? tk.pen_z(cm, i) : -INFINITY, i < tk.np ? tk.pen_tok(cm, i) : 0);
+  flush();
+  acc = wave_sum(acc);
+  if (lane() == 0) a.ws.nexcl[(size_t)g * kWaves + wave()] = acc;
+  // the staged window tokens: one reservation per wave, then to the slots
+  int base = 0;
+  if (lane() == 0 && cn > 0) base = lds_fetch_add(&cm.cand_n, cn);
+  base = lane_value(base, 0);
+  if (cn > kNucCandWave || base + cn > capc) {
+    if (lane() == 0) over = 1;
+  } else {
+    double* cz = a.ws.cz + (size_t)g * capc;
+    int32_t* ci = a.ws.ci + (size_t)g * capc;
+    for (int i = lane(); i < cn; i += kWave) {
+      cz[base + i] = nuc_p(ys(cs[i].d), nr, tab);
+      ci[base + i] = (int)cc[i];
     }
   }
-  for (int i = 0; i < tk.np; ++i) {
-    const double z = tk.pen_z(cm, i);
-    if (z > -INFINITY) {
-      const int b = af.bin(z);
-      if (b < nr.dlo) {
-        ex += nuc_p(ys(z), nr, tab);
-      } else if (b <= nr.dhi) {
-        const int slot = lds_fetch_add(&cm.cand_n, 1);
-        if (slot < capc) {
-          cz[slot] = nuc_p(ys(z), nr, tab);
-          ci[slot] = tk.pen_tok(cm, i);
-        }
-      }
-    }
-  }
-  ex = wave_sum(ex);
-  if (lane() == 0) a.ws.nexcl[(size_t)g * kWaves + wave()] = ex;
   wg_barrier();
-  if (threadIdx.x == 0) a.ws.ncand[g] = cm.cand_n > capc ? -1 : cm.cand_n;
+  if (threadIdx.x == 0) a.ws.ncand[g] = over ? -1 : cm.cand_n;
 }
 
 template <typename TIn, bool VEC>
@@ -1670,9 +1733,13 @@ __global__ __launch_bounds__(kThreads) void k_nuc_final(SampleArgs a) {
       for (int w = 0; w < kWaves; ++w) wsum += sw[0][w];
       double dl = 0.0;
       for (int s = lane(); s < nseg; s += kWave) dl += a.ws.nexcl[(size_t)row * nseg + s];
-      const uint64_t below_and_in = to_fx(uniform(wave_sum(dl))) + wsum;
-      const uint64_t total = kFxOne;
-      const uint64_t above = below_and_in < total ? total - below_and_in : 0ull;
+      const double side = uniform(wave_sum(dl));
+      const bool abv = nr.above != 0;
+      uint64_t above = to_fx(side);
+      if (!abv) {
+        const uint64_t below_and_in = above + wsum;
+        above = below_and_in < kFxOne ? kFxOne - below_and_in : 0ull;
+      }
       const uint64_t target = topp_target(rp.top_p);
       SelOut r{false, true, 0, 0};
       if (above < target)
@@ -1681,30 +1748,38 @@ __global__ __launch_bounds__(kThreads) void k_nuc_final(SampleArgs a) {
       if (!r.found || r.giveup) {
         general = true;
       } else {
-        // candidates past the cut, by segment (fixed point)
+        // by segment (fixed point): the kept candidates when the side
+        // summed is above the window, else the candidates past the cut
         Hist& h = next_hist(fs, hgen);
 #pragma unroll
         for (int q = 0; q < kPerT; ++q) {
           if (((rc.valid >> q) & 1u) && rc.w[q] != 0ull) {
             const uint64_t k = pkey_of(rc.v[q]);
-            if (!(k > r.key || (k == r.key && rc.idx[q] <= r.idx))) lds_add(&h.mass[rc.idx[q] / G::kSeg], rc.w[q]);
+            const bool kept = k > r.key || (k == r.key && rc.idx[q] <= r.idx);
+            if (kept == abv) lds_add(&h.mass[rc.idx[q] / G::kSeg], rc.w[q]);
           }
         }
         wg_barrier();
-        // kept mass per segment: its share of the normaliser less what lies
+        // kept mass per segment: the mass above the window plus the kept
+        // candidates, or the segment's share of the normaliser less the mass
         // below the window and the candidates past the cut
         const int nsv = (V + G::kSeg - 1) / G::kSeg;
-        SegLoad sg;
-        load_segs(a, row, nsv, sg);
-        double ms[kSegPerLane], lex;
-        seg_norm(sg, tab, ms, &lex);
+        double ms[kSegPerLane];
+        if (!abv) {
+          SegLoad sg;
+          load_segs(a, row, nsv, sg);
+          double lex;
+          seg_norm(sg, tab, ms, &lex);
+        }
         double kk[kSegPerLane], ks = 0.0;
 #pragma unroll
         for (int j = 0; j < kSegPerLane; ++j) {
           const int s = kSegPerLane * lane() + j;
           kk[j] = 0.0;
           if (s < nsv) {
-            kk[j] = ms[j] * nr.invS - a.ws.nexcl[(size_t)row * nseg + s] - (double)h.mass[s] * (1.0 / kFxScale);
+            const double side_s = a.ws.nexcl[(size_t)row * nseg + s];
+            const double cand_s = (double)h.mass[s] * (1.0 / kFxScale);
+            kk[j] = abv ? side_s + cand_s : ms[j] * nr.invS - side_s - cand_s;
             if (!(kk[j] > 0.0)) kk[j] = 0.0;
           }
           ks += kk[j];
@@ -1742,7 +1817,7 @@ __global__ __launch_bounds__(kThreads) void k_nuc_final(SampleArgs a) {
           constexpr int kPer = G::kSeg / kThreads;
           const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
           const YScale ys{rp.T, 1.0 / rp.T};
-          const Affine af{nr.zlo, nr.scale, kNucBins};
+          const NucBin nb(nr);
           const int q0 = kPer * (int)threadIdx.x;
           double e[kPer], es = 0.0;
 #pragma unroll
@@ -1753,7 +1828,7 @@ __global__ __launch_bounds__(kThreads) void k_nuc_final(SampleArgs a) {
               double z = (double)x[p];
               if (rp.pen_active && ((fs.segbits[(q0 + q) >> 5] >> ((q0 + q) & 31)) & 1u)) z = penalize(z, rp.pen);
               if (z > -INFINITY) {
-                const int b = af.bin(z);
+                const int b = nb(z);
                 if (b >= nr.dlo) {
                   const double pz = nuc_p(ys(z), nr, tab);
                   const uint64_t k = pkey_of(pz);
