@@ -120,3 +120,20 @@ def test_bulk_uniform_draws_match_scalar_draws():
     x = [a.random() for _ in range(6)]
     assert np.array_equal(np.array(x), b.random(6))
     assert a.bit_generator.state == b.bit_generator.state
+
+
+def test_nucleus_hint_only_for_high_top_p_rows_without_top_k():
+    """The hint is set when some non-greedy row has no top-k (0 or >= V) and
+    0.98 <= top_p < 1; it never depends on other rows."""
+    from pagellm_amd import _native
+
+    def hint(rows, V=100):
+        return S._nucleus_hint(*S._pack_params(rows)[:3], V)
+
+    assert hint([SamplingParams(top_p=0.99)]) == _native.PLH_SAMPLE_NUCLEUS
+    assert hint([SamplingParams(top_p=0.98, top_k=100)]) == _native.PLH_SAMPLE_NUCLEUS  # top_k >= V is off
+    assert hint([SamplingParams(top_p=0.97)]) == 0
+    assert hint([SamplingParams(top_p=1.0)]) == 0
+    assert hint([SamplingParams(top_p=0.99, top_k=40)]) == 0
+    assert hint([SamplingParams(top_p=0.99, temperature=0.0)]) == 0
+    assert hint([SamplingParams(), SamplingParams(top_p=0.995)]) == _native.PLH_SAMPLE_NUCLEUS
