@@ -37,6 +37,7 @@ struct NucRow {
   int above;     // 1: nexcl sums the tokens above the window (fewer than those below)
 };
 constexpr int kNucActive = 1;
+constexpr int kNucPenWords = 512;  // bitmap words of one chunk (16384 float tokens)
 constexpr int kNucBins = 2048;
 
 // Workspace of the two-launch fast path, carved from one device buffer.
@@ -50,6 +51,7 @@ struct ChunkWs {
   uint32_t* ncnt;   // [B * kNucBins] nucleus path: token counts per y bin
   double* nexcl;    // [B * C * 8] nucleus path: per-segment mass on one side of the candidate bins
   int32_t* ncand;   // [B * C] nucleus path: candidates per chunk (-1: over capacity)
+  uint32_t* npen;   // [B * C * kNucPenWords] nucleus path: each chunk's penalised-token bitmap
   int C;            // chunks per row
   int capc;         // candidate slots per chunk
 };

@@ -579,6 +579,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   if (rp.pen_active) {
     const uint32_t pb = chunk_pbits<TIn>(a, rp, c0, cm);
     if (set_aside_penalised<TIn>(tk, pb, rp.pen, c0, cm)) flags = kChunkIncomplete;
+    if (rp.nucleus) {  // the nucleus kernels read the chunk's bitmap from here
+      uint32_t* out = a.ws.npen + (size_t)g * kNucPenWords;
+      for (int w = threadIdx.x; w < G::kChunk / 32; w += kThreads) out[w] = cm.bitmap[w];
+    }
   }
   WavePart* wp = a.ws.part + (size_t)g * kWaves + wave();
   if (rp.greedy) {
@@ -1399,6 +1403,22 @@ struct NucBin {
   }
 };
 
+// The calling lane's penalty bits (as chunk_pbits) from the chunk bitmap
+// the first pass wrote.
+template <typename TIn>
+__device__ __forceinline__ uint32_t nuc_pbits(const SampleArgs& a, int g) {
+  using G = Geo<TIn>;
+  const uint32_t* bm = a.ws.npen + (size_t)g * kNucPenWords;
+  uint32_t pb = 0;
+  const int q0 = wave() * G::kSeg + lane() * G::kVW;
+#pragma unroll
+  for (int j = 0; j < kU; ++j) {
+    const int q = q0 + j * G::kSpan;
+    pb |= ((bm[q >> 5] >> (q & 31)) & ((1u << G::kVW) - 1u)) << (G::kVW * j);
+  }
+  return pb;
+}
+
 // p of a nucleus row's token: exp(y - ymax) / S.
 __device__ __forceinline__ double nuc_p(double y, const NucRow& nr, const double* tab) {
   return fast_exp_neg(y - nr.ymax, tab) * nr.invS;
@@ -1424,8 +1444,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   if (rp.pen_active) {
     // the first pass set aside the same tokens without overflow, or the
     // row would not be here
-    const uint32_t pb = chunk_pbits<TIn>(a, rp, c0, cm);
-    set_aside_penalised<TIn>(tk, pb, rp.pen, c0, cm);
+    set_aside_penalised<TIn>(tk, nuc_pbits<TIn>(a, g), rp.pen, c0, cm);
   }
   wg_barrier();
   const NucBin nb(nr);
@@ -1602,10 +1621,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     cm.cand_n = 0;
     over = 0;
   }
-  if (rp.pen_active) {
-    const uint32_t pb = chunk_pbits<TIn>(a, rp, c0, cm);
-    set_aside_penalised<TIn>(tk, pb, rp.pen, c0, cm);
-  }
+  if (rp.pen_active) set_aside_penalised<TIn>(tk, nuc_pbits<TIn>(a, g), rp.pen, c0, cm);
   wg_barrier();
   const YScale ys{rp.T, 1.0 / rp.T};
   const NucBin nb(nr);
@@ -1943,7 +1959,8 @@ size_t fast_ws_bytes(int B, int V, bool f64) {
   const size_t C = (size_t)chunks_of(V, f64), cap = (size_t)capc_of((int)C), n = (size_t)B * C;
   return up256(n * kWaves * sizeof(WavePart)) + 2 * up256(n * kWaves * sizeof(double)) + up256(n * cap * sizeof(double)) +
          up256(n * cap * sizeof(int32_t)) + up256((size_t)B * sizeof(NucRow)) +
-         up256((size_t)B * kNucBins * sizeof(uint32_t)) + up256(n * kWaves * sizeof(double)) + up256(n * sizeof(int32_t));
+         up256((size_t)B * kNucBins * sizeof(uint32_t)) + up256(n * kWaves * sizeof(double)) + up256(n * sizeof(int32_t)) +
+         up256(n * kNucPenWords * sizeof(uint32_t));
 }
 
 ChunkWs fast_ws_layout(void* base, int B, int V, bool f64) {
@@ -1969,6 +1986,8 @@ ChunkWs fast_ws_layout(void* base, int B, int V, bool f64) {
   w.nexcl = reinterpret_cast<double*>(p);
   p += up256(n * kWaves * sizeof(double));
   w.ncand = reinterpret_cast<int32_t*>(p);
+  p += up256(n * sizeof(int32_t));
+  w.npen = reinterpret_cast<uint32_t*>(p);
   return w;
 }
 
