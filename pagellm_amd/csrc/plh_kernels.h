@@ -12,12 +12,12 @@ namespace plh {
 struct WavePart {
   double zmax;    // largest finite penalised logit of the segment (-inf if none)
   double umax;    // bound on the tokens not kept as candidates: all are below it
+                  // (nucleus rows: the smallest finite penalised logit, +inf if none)
   double best_z;  // greedy rows: the segment's argmax value ...
   int best_idx;   // ... and its token id
   int end;        // candidate rows: end of the wave's slots in its chunk's list
                   // (the chunk's candidate count is the largest end)
   int flags;      // kChunkIncomplete: the row needs the general pipeline
-  double zmin;    // nucleus rows: smallest finite penalised logit (+inf if none)
 };
 constexpr int kChunkIncomplete = 1;
 

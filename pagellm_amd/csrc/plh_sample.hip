@@ -558,7 +558,7 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
 // temperature chunks need no workgroup barrier; candidate chunks need the
 // few of one value histogram.  Per row mode: greedy argmax, candidates,
 // segment partials of the normaliser.
-template <typename TIn, bool VEC>
+template <typename TIn, bool VEC, bool NUC>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_sample_chunks(SampleArgs a) {
   using G = Geo<TIn>;
   __shared__ ChunkSmem cm;
@@ -570,7 +570,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
   ChunkToks<TIn> tk;
   load_chunk<TIn, VEC>(x, a.V, c0, tk.v);
-  const bool cands = rp.topk || (rp.topp && !rp.nucleus);
+  const bool cands = rp.topk || (rp.topp && !(NUC && rp.nucleus));
   if (cands) {  // ordered before use by the first barrier of chunk_candidates
     for (int b = threadIdx.x; b < kHB + 1; b += kThreads) cm.hcnt[b] = 0u;
     if (threadIdx.x == 0) cm.cand_n = 0;
@@ -579,7 +579,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   if (rp.pen_active) {
     const uint32_t pb = chunk_pbits<TIn>(a, rp, c0, cm);
     if (set_aside_penalised<TIn>(tk, pb, rp.pen, c0, cm)) flags = kChunkIncomplete;
-    if (rp.nucleus) {  // the nucleus kernels read the chunk's bitmap from here
+    if (NUC && rp.nucleus) {  // the nucleus kernels read the chunk's bitmap from here
       uint32_t* out = a.ws.npen + (size_t)g * kNucPenWords;
       for (int w = threadIdx.x; w < G::kChunk / 32; w += kThreads) out[w] = cm.bitmap[w];
     }
@@ -617,7 +617,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   for (int i = 0; i < tk.np; ++i) lmax = fmax(lmax, tk.pen_z(cm, i));
   if (cands) chunk_candidates<TIn>(tk, lmax, a, rp, g, c0, flags, wp, cm);
   else if (lane() == 0) wp->flags = flags;
-  if (rp.nucleus) {  // the lower edge of the row's y histogram
+  if (NUC && rp.nucleus && g == row * C)  // the row's count histogram, filled by k_nuc_hist
+    for (int b = threadIdx.x; b < kNucBins; b += kThreads) a.ws.ncnt[(size_t)row * kNucBins + b] = 0u;
+  if (NUC && rp.nucleus) {  // the range of the row's count histogram
     TIn lmn = (TIn)INFINITY;
     tk.new_pass();
 #pragma unroll
@@ -633,7 +635,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     zmn = wave_min(zmn);
     const double zmx = wave_max(lmax);
     if (lane() == 0) {
-      wp->zmin = zmn;
+      wp->umax = zmn;  // the nucleus kernels' lower range edge
       wp->zmax = zmx;
     }
   }
@@ -1285,17 +1287,14 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, RegCands& r
   return FastOut{draw_kept(rc, V, rp.u, fs, hgen), false, 0.0};
 }
 
-template <typename TIn, bool VEC>
+template <typename TIn, bool VEC, bool NUC>
 __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   __shared__ SmemAll sm;
   FastSmem& fs = sm.f;
   const int row = blockIdx.x;
   const RowParams rp = load_row_params(a, row);
   init_exp_table_wave(fs.exp_tab[wave()]);
-  // a nucleus row is handed on below; until then (and for good when it is
-  // finished here) the nucleus kernels leave it alone
-  if (rp.nucleus && threadIdx.x == 0) a.ws.nrow[row].state = 0;
-  const bool cands = !rp.greedy && (rp.topk || (rp.topp && !rp.nucleus));
+  const bool cands = !rp.greedy && (rp.topk || (rp.topp && !(NUC && rp.nucleus)));
   if (cands) {  // ordered before their first use by the first barrier
     for (int b = threadIdx.x; b < kHB; b += kThreads) {
       fs.h[0].cnt[b] = 0u;
@@ -1323,31 +1322,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   bool general = ps.flags != 0;
   int id = 0;
   PipeIn pin{false, 0.0, false, 0.0, false, 0.0};  // what the fast path already knows of the row
-  if (!general && rp.nucleus) {  // the nucleus kernels finish the row
-    uint32_t* cnt = a.ws.ncnt + (size_t)row * kNucBins;
-    for (int b = threadIdx.x; b < kNucBins; b += kThreads) cnt[b] = 0u;
-    if (wave() == 0) {
-      // the count histogram spans the row's finite penalised logits
-      const WavePart* pp = a.ws.part + (size_t)row * a.ws.C * kWaves;
-      double lo = INFINITY, hi = -INFINITY;
-      for (int j = lane(); j < a.ws.C * kWaves; j += kWave) {
-        lo = fmin(lo, pp[j].zmin);
-        hi = fmax(hi, pp[j].zmax);
-      }
-      lo = wave_min(lo);
-      hi = wave_max(hi);
-      if (lane() == 0) {
-        const double scale = (double)kNucBins / (hi - lo);
-        NucRow& nr = a.ws.nrow[row];
-        nr.zlo = lo;
-        nr.scale = scale;
-        // one distinct finite value, or none: the general pipeline
-        nr.general = (hi - lo > 0.0 && hi - lo < INFINITY && scale < INFINITY) ? 0 : 1;
-        nr.state = kNucActive;
-      }
-    }
-    return;
-  }
+  if (NUC && !general && rp.nucleus) return;  // the nucleus kernels finish the row
   if (general) {
   } else if (rp.greedy) {
     id = ps.best.i;
@@ -1373,17 +1348,19 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
 // (top_p 0.99 over a Zipf-like distribution keeps ~90% of it), more than
 // any candidate list holds.  With the caller's hint they take passes over
 // all chunks instead of one workgroup per row: k_sample_chunks leaves the
-// segment partials of the normaliser and each wave's smallest and largest
-// finite logit, k_sample_final spreads kNucBins affine bins over the row's
-// range of z, then
-//   k_nuc_hist    counts the row's tokens per bin;
+// segment partials of the normaliser, each wave's smallest and largest
+// finite logit and (penalised rows) each chunk's bitmap of penalised
+// tokens, and zeroes the row's counts; k_sample_final leaves the row alone
+// unless a chunk could not set its penalised tokens aside; then
+//   k_nuc_hist    spreads kNucBins affine bins over the row's range of z and
+//                 counts the row's tokens per bin;
 //   k_nuc_window  bounds each bin's mass by its count and the exp of its
 //                 edges, which brackets the top-p cut (sampling.py:82-90) in a
 //                 window of bins: the bins below it hold at most 1 - top_p
 //                 of the mass (dropped), those above it more than that below
 //                 them (kept);
-//   k_nuc_cands   writes the window's tokens as candidates and sums the mass
-//                 below the window per segment;
+//   k_nuc_cands   writes the window's tokens as candidates and sums, per
+//                 segment, the mass on the row's smaller side of the window;
 //   k_nuc_final   finds the cut among the candidates in (p desc, idx asc)
 //                 order, starting from the mass above the window, then draws
 //                 (sampling.py:94-98): the segment where the kept mass
@@ -1434,8 +1411,34 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const int row = g / C;
   const RowParams rp = load_row_params(a, row);
   if (!rp.nucleus) return;
-  const NucRow nr = a.ws.nrow[row];
-  if (nr.state != kNucActive || nr.general != 0) return;
+  // the row's range of finite penalised logits and the first pass's flags
+  // (each wave reads all the row's parts)
+  const WavePart* pp = a.ws.part + (size_t)row * C * kWaves;
+  double lo = INFINITY, hi = -INFINITY;
+  int fl = 0;
+  for (int j = lane(); j < C * kWaves; j += kWave) {
+    lo = fmin(lo, pp[j].umax);  // nucleus rows: the wave's smallest finite logit
+    hi = fmax(hi, pp[j].zmax);
+    fl |= pp[j].flags;
+  }
+  lo = uniform(wave_min(lo));
+  hi = uniform(wave_max(hi));
+  fl = uniform(wave_max(fl));
+  NucRow nr;
+  nr.zlo = lo;
+  nr.scale = (double)kNucBins / (hi - lo);
+  // one distinct finite value, or none: the general pipeline (k_nuc_final)
+  const bool degenerate = !(hi - lo > 0.0 && hi - lo < INFINITY && nr.scale < INFINITY);
+  if (g == row * C && threadIdx.x == 0) {
+    NucRow& out = a.ws.nrow[row];
+    out.zlo = nr.zlo;
+    out.scale = nr.scale;
+    out.general = degenerate ? 1 : 0;
+    // a chunk that could not set its penalised tokens aside sent the row
+    // to the general pipeline in k_sample_final already
+    out.state = fl != 0 ? 0 : kNucActive;
+  }
+  if (fl != 0 || degenerate) return;
   const int c0 = (g - row * C) * G::kChunk;
   const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
   ChunkToks<TIn> tk;
@@ -2007,20 +2010,23 @@ hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, int num_c
   (void)num_cu;
   const int total = a.B * a.ws.C;
   const dim3 gf(a.B), block(kThreads);
-  if (vec) {
-    if (f64) hipLaunchKernelGGL((k_sample_chunks<double, true>), dim3(total), block, 0, s, a);
-    else hipLaunchKernelGGL((k_sample_chunks<float, true>), dim3(total), block, 0, s, a);
-  } else {
-    if (f64) hipLaunchKernelGGL((k_sample_chunks<double, false>), dim3(total), block, 0, s, a);
-    else hipLaunchKernelGGL((k_sample_chunks<float, false>), dim3(total), block, 0, s, a);
-  }
+  // the nucleus code is compiled only into the instantiations the hint selects
+  using K = void (*)(SampleArgs);
+  const K chunks[2][2][2] = {{{k_sample_chunks<float, false, false>, k_sample_chunks<float, false, true>},
+                              {k_sample_chunks<float, true, false>, k_sample_chunks<float, true, true>}},
+                             {{k_sample_chunks<double, false, false>, k_sample_chunks<double, false, true>},
+                              {k_sample_chunks<double, true, false>, k_sample_chunks<double, true, true>}}};
+  const K finals[2][2][2] = {{{k_sample_final<float, false, false>, k_sample_final<float, false, true>},
+                              {k_sample_final<float, true, false>, k_sample_final<float, true, true>}},
+                             {{k_sample_final<double, false, false>, k_sample_final<double, false, true>},
+                              {k_sample_final<double, true, false>, k_sample_final<double, true, true>}}};
+  const int nuc = a.nucleus ? 1 : 0;
+  hipLaunchKernelGGL(chunks[f64][vec][nuc], dim3(total), block, 0, s, a);
   if (between != nullptr) {
     const hipError_t e = hipEventRecord(between, s);
     if (e != hipSuccess) return e;
   }
-  auto final_ = f64 ? (vec ? k_sample_final<double, true> : k_sample_final<double, false>)
-                    : (vec ? k_sample_final<float, true> : k_sample_final<float, false>);
-  hipLaunchKernelGGL(final_, gf, block, 0, s, a);
+  hipLaunchKernelGGL(finals[f64][vec][nuc], gf, block, 0, s, a);
   if (a.nucleus) {
     auto hist = f64 ? (vec ? k_nuc_hist<double, true> : k_nuc_hist<double, false>)
                     : (vec ? k_nuc_hist<float, true> : k_nuc_hist<float, false>);
