@@ -1322,7 +1322,34 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   bool general = ps.flags != 0;
   int id = 0;
   PipeIn pin{false, 0.0, false, 0.0, false, 0.0};  // what the fast path already knows of the row
-  if (NUC && !general && rp.nucleus) return;  // the nucleus kernels finish the row
+  if (NUC && rp.nucleus) {
+    if (general) {
+      if (threadIdx.x == 0) a.ws.nrow[row].state = 0;  // finished here: the nucleus kernels skip it
+    } else {
+      // the nucleus kernels finish the row; its count histogram spans the
+      // row's finite penalised logits
+      if (wave() == 0) {
+        const WavePart* pp = a.ws.part + (size_t)row * a.ws.C * kWaves;
+        double lo = INFINITY, hi = -INFINITY;
+        for (int j = lane(); j < a.ws.C * kWaves; j += kWave) {
+          lo = fmin(lo, pp[j].umax);  // nucleus rows: the wave's smallest finite logit
+          hi = fmax(hi, pp[j].zmax);
+        }
+        lo = wave_min(lo);
+        hi = wave_max(hi);
+        if (lane() == 0) {
+          const double scale = (double)kNucBins / (hi - lo);
+          NucRow& nr = a.ws.nrow[row];
+          nr.zlo = lo;
+          nr.scale = scale;
+          // one distinct finite value, or none: the general pipeline (k_nuc_final)
+          nr.general = (hi - lo > 0.0 && hi - lo < INFINITY && scale < INFINITY) ? 0 : 1;
+          nr.state = kNucActive;
+        }
+      }
+      return;
+    }
+  }
   if (general) {
   } else if (rp.greedy) {
     id = ps.best.i;
@@ -1350,10 +1377,10 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
 // all chunks instead of one workgroup per row: k_sample_chunks leaves the
 // segment partials of the normaliser, each wave's smallest and largest
 // finite logit and (penalised rows) each chunk's bitmap of penalised
-// tokens, and zeroes the row's counts; k_sample_final leaves the row alone
-// unless a chunk could not set its penalised tokens aside; then
-//   k_nuc_hist    spreads kNucBins affine bins over the row's range of z and
-//                 counts the row's tokens per bin;
+// tokens, and zeroes the row's counts; k_sample_final spreads kNucBins
+// affine bins over the row's range of z (or finishes the row itself when a
+// chunk could not set its penalised tokens aside); then
+//   k_nuc_hist    counts the row's tokens per bin;
 //   k_nuc_window  bounds each bin's mass by its count and the exp of its
 //                 edges, which brackets the top-p cut (sampling.py:82-90) in a
 //                 window of bins: the bins below it hold at most 1 - top_p
@@ -1411,38 +1438,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const int row = g / C;
   const RowParams rp = load_row_params(a, row);
   if (!rp.nucleus) return;
-  // the row's range of finite penalised logits and the first pass's flags
-  // (each wave reads all the row's parts)
-  const WavePart* pp = a.ws.part + (size_t)row * C * kWaves;
-  double lo = INFINITY, hi = -INFINITY;
-  int fl = 0;
-  for (int j = lane(); j < C * kWaves; j += kWave) {
-    lo = fmin(lo, pp[j].umax);  // nucleus rows: the wave's smallest finite logit
-    hi = fmax(hi, pp[j].zmax);
-    fl |= pp[j].flags;
-  }
-  lo = uniform(wave_min(lo));
-  hi = uniform(wave_max(hi));
-  fl = uniform(wave_max(fl));
-  NucRow nr;
-  nr.zlo = lo;
-  nr.scale = (double)kNucBins / (hi - lo);
-  // one distinct finite value, or none: the general pipeline (k_nuc_final)
-  const bool degenerate = !(hi - lo > 0.0 && hi - lo < INFINITY && nr.scale < INFINITY);
-  if (g == row * C && threadIdx.x == 0) {
-    NucRow& out = a.ws.nrow[row];
-    out.zlo = nr.zlo;
-    out.scale = nr.scale;
-    out.general = degenerate ? 1 : 0;
-    // a chunk that could not set its penalised tokens aside sent the row
-    // to the general pipeline in k_sample_final already
-    out.state = fl != 0 ? 0 : kNucActive;
-  }
-  if (fl != 0 || degenerate) return;
   const int c0 = (g - row * C) * G::kChunk;
   const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
   ChunkToks<TIn> tk;
-  load_chunk<TIn, VEC>(x, a.V, c0, tk.v);
+  load_chunk<TIn, VEC>(x, a.V, c0, tk.v);  // in flight while the row's state is read
+  const NucRow nr = a.ws.nrow[row];
+  if (nr.state != kNucActive || nr.general != 0) return;
   for (int b = threadIdx.x; b < kNucBins; b += kThreads) nh[b] = 0u;
   if (rp.pen_active) {
     // the first pass set aside the same tokens without overflow, or the
@@ -1823,13 +1824,10 @@ __global__ __launch_bounds__(kThreads) void k_nuc_final(SampleArgs a) {
           const int kstar = uniform(lane_value(kl, L));
           const double before = uniform(lane_value(bl, L));
           const int s0 = kstar * G::kSeg;
-          if (rp.pen_active) {
-            for (int w = threadIdx.x; w < G::kSeg / 32; w += kThreads) fs.segbits[w] = 0u;
-            wg_barrier();
-            for (int64_t hh = rp.h0 + threadIdx.x; hh < rp.h1; hh += kThreads) {
-              const int off = a.hist_ids[hh] - s0;
-              if ((unsigned)off < (unsigned)G::kSeg) lds_or(&fs.segbits[off >> 5], 1u << (off & 31));
-            }
+          if (rp.pen_active) {  // the segment's words of its chunk's penalty bitmap
+            const uint32_t* bm = a.ws.npen + ((size_t)row * C + kstar / kWaves) * kNucPenWords +
+                                 (kstar % kWaves) * (G::kSeg / 32);
+            for (int w = threadIdx.x; w < G::kSeg / 32; w += kThreads) fs.segbits[w] = bm[w];
             wg_barrier();
           }
           // thread t holds tokens s0 + kPer*t + q, in vocabulary order
