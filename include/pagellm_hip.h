@@ -49,9 +49,9 @@ extern "C" {
                                    slots that grow in place (plh_append_ids) */
 #define PLH_SAMPLE_NUCLEUS 4 /* performance hint, same results: rows with no
                                 top-k and top_p >= 0.98 (nuclei that hold most
-                                of the vocabulary) take a three-pass path over
-                                all chunks instead of the per-row general
-                                pipeline; costs three extra launches */
+                                of the vocabulary) take three streaming passes
+                                over all chunks instead of the per-row general
+                                pipeline; costs four extra launches */
 
 /* plh_set_option options */
 #define PLH_OPT_KERNEL_TIMING 1 /* value 1: bracket the fast path's kernels with
@@ -72,8 +72,9 @@ const char* plh_last_error(const plh_ctx* ctx);
  * restores the context's own stream. */
 int plh_set_stream(plh_ctx* ctx, void* stream);
 int plh_set_option(plh_ctx* ctx, int option, int64_t value);
-/* Rows the fast path's merge kernel finished with the general row-wise
- * pipeline, cumulative since plh_create (waits for queued work). */
+/* Rows the fast path (its merge kernel or the nucleus kernels) finished with
+ * the general row-wise pipeline, cumulative since plh_create (waits for
+ * queued work). */
 int plh_fallback_rows(plh_ctx* ctx, int64_t* out);
 /* While PLH_OPT_KERNEL_TIMING is on: device time of the fast path's
  * streaming kernel and merge kernel summed over the plh_sample calls made

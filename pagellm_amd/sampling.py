@@ -122,7 +122,7 @@ NUCLEUS_TOP_P = 0.98  # rows with no top-k from this top_p up may take the nucle
 def _nucleus_hint(t: np.ndarray, k: np.ndarray, p: np.ndarray, V: int) -> int:
     """``PLH_SAMPLE_NUCLEUS`` when some row is non-greedy with no top-k and
     ``NUCLEUS_TOP_P <= top_p < 1``: such nuclei hold most of the vocabulary,
-    which the three-pass path handles faster than the per-row general
+    which the multi-pass nucleus kernels handle faster than the per-row general
     pipeline.  The sampled ids do not depend on the hint."""
     rows = (t != 0) & ((k <= 0) | (k >= V)) & (p >= NUCLEUS_TOP_P) & (p < 1.0)
     return _native.PLH_SAMPLE_NUCLEUS if bool(rows.any()) else 0
