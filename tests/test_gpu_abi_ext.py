@@ -132,3 +132,38 @@ def test_pinned_staging_and_queued_copy():
             dev.free()
     finally:
         c.close()
+
+
+def test_nucleus_hint_changes_the_path_not_the_ids():
+    """PLH_SAMPLE_NUCLEUS only moves rows with no top-k and top_p >= 0.98
+    from the general pipeline to the nucleus kernels: the same batch (a
+    Zipf-like row set mixed with greedy, top-k and plain top-p rows, CSR and
+    span histories) gives the same ids with and without it, and only
+    without it do the high-top_p rows fall back."""
+    g = np.random.default_rng(8)
+    B, V = 10, 60000
+    ranks = 1 + np.stack([g.permutation(V) for _ in range(B)])
+    x = (-np.log(ranks) + g.normal(0, 0.3, (B, V))).astype(np.float32)
+    params = [SamplingParams(top_p=0.99, repetition_penalty=1.05)] * 6 + [
+        SamplingParams(temperature=0.0), SamplingParams(top_k=50), SamplingParams(top_p=0.9),
+        SamplingParams(top_p=0.995, temperature=0.8)]
+    u = g.random(B)
+    hists = [g.integers(0, V, 700).astype(np.int32) for _ in range(B)]
+    ids = np.concatenate(hists)
+    off = np.concatenate([[0], np.cumsum([h.size for h in hists])]).astype(np.int64)
+    c = _native.Context(0)
+    f0 = c.fallback_rows()
+    plain = _sample(c, x, params, u, ids, off, 0)
+    f1 = c.fallback_rows()
+    hinted = _sample(c, x, params, u, ids, off, _native.PLH_SAMPLE_NUCLEUS)
+    f2 = c.fallback_rows()
+    assert np.array_equal(plain, hinted)
+    # the seven top_p >= 0.98 rows leave the general pipeline; the top_p 0.9
+    # row (a nucleus too wide for the candidate slots) falls back either way
+    assert (f1 - f0) - (f2 - f1) == 7, (f1 - f0, f2 - f1)
+    spans = np.stack([off[:-1], off[1:]], axis=1).reshape(-1)
+    assert np.array_equal(hinted, _sample(c, x, params, u, ids, spans,
+                                          _native.PLH_SAMPLE_NUCLEUS | _native.PLH_SAMPLE_HIST_SPANS))
+    for b in range(B):
+        ref = oracle.sample(x[b], params[b], u[b], hists[b])
+        assert hinted[b] == ref or min(oracle.sampler.sample_boundary_gaps(x[b], params[b], u[b], hists[b])) < 1e-6
