@@ -72,11 +72,63 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline_child(workload: str, rows: int, reps: int) -> None:
+def _parity_rows(w, rows, gpu_ids):
+    """Oracle ids for the given rows against the GPU's, with the boundary
+    gauges for every row: greedy rows must agree exactly; a sampled row may
+    differ only if its uniform lies within 1e-6 of a CDF boundary or its
+    top-p cut within 1e-12 of flipping."""
+    import oracle
+    from oracle.sampler import sample_boundary_gaps
+
+    greedy = mism = explained = in_band = 0
+    greedy_exact = True
+    for r in rows:
+        prm, x, ctx, u = w["params"][r], w["logits"][r], w["contexts"][r], w["uniforms"][r]
+        ref = oracle.sample(x, prm, u, ctx)
+        if prm.greedy:
+            greedy += 1
+            if int(gpu_ids[r]) != ref:
+                greedy_exact = False
+                mism += 1
+            continue
+        g_topp, g_draw = sample_boundary_gaps(x, prm, u, ctx)
+        band = g_topp < 1e-12 or g_draw < 1e-6
+        in_band += band
+        if int(gpu_ids[r]) != ref:
+            mism += 1
+            explained += band
+    return {"rows": len(rows), "greedy_rows": greedy, "greedy_exact": greedy_exact, "mismatches": mism,
+            "boundary_cases": explained, "rows_in_boundary_band": in_band,
+            "unexplained_mismatches": mism - explained}
+
+
+def _parity_verify(w, toks, nacc):
+    import numpy as np
+
+    import oracle
+    from oracle.sampler import verify_boundary_gap
+
+    rt, rn = oracle.verify_batch(w["p"], w["q"], w["draft"], w["accept_u"], w["resample_u"])
+    mism = explained = in_band = 0
+    for b in range(len(rn)):
+        gap = verify_boundary_gap(w["p"][b], w["q"][b], [int(t) for t in w["draft"][b]], w["accept_u"][b],
+                                  w["resample_u"][b])
+        band = gap < 1e-6
+        in_band += band
+        if int(nacc[b]) != int(rn[b]) or not np.array_equal(toks[b], rt[b]):
+            mism += 1
+            explained += band
+    return {"rows": int(len(rn)), "accept_counts_exact": bool(np.array_equal(nacc, rn)), "mismatches": mism,
+            "boundary_cases": explained, "rows_in_boundary_band": in_band, "unexplained_mismatches": mism - explained}
+
+
+def cpu_baseline_child(workload: str, rows: int, reps: int, ids_path: str | None) -> None:
     """Runs in a fresh process that never touches the GPU, BLAS pinned to one
     thread: the oracle over the sample on one pinned core (the engine's
     single thread), then the same sample split row-wise over a pool of
-    processes, one per allowed core (at most 16)."""
+    processes, one per allowed core (at most 16).  Untimed afterwards: the
+    GPU ids of every configuration the parent measured (ids_path) against
+    the oracle's on the same inputs and uniforms."""
     global _POOL_JOB
     cores = sorted(os.sched_getaffinity(0))
     os.sched_setaffinity(0, {cores[0]})
@@ -120,6 +172,24 @@ def cpu_baseline_child(workload: str, rows: int, reps: int) -> None:
     if not np.array_equal(ids_n, np.asarray(ids1)):
         raise RuntimeError("the pooled CPU baseline disagrees with the one-core run")
     pmed = float(np.median(ptimes))
+    parity = None
+    if ids_path:
+        got = np.load(ids_path, allow_pickle=False)
+        parity = {}
+        if workload in got.files:  # the headline: the timed rows' oracle ids against the GPU's
+            gpu = got[workload]
+            ref = np.asarray(ids1)
+            rows_all = [int(i) for i in sel]
+            parity[workload] = _parity_rows(w, rows_all, gpu)
+            assert parity[workload]["mismatches"] == int(np.sum(gpu[sel] != ref))
+        for name in ("char65", "zipf32k", "zipf152k"):
+            if name in got.files and name != workload:
+                wn = workloads.WORKLOADS[name]()
+                Bn = wn["logits"].shape[0]
+                rows_n = list(range(Bn)) if Bn <= 256 else list(range(0, Bn, Bn // 128))
+                parity[name] = _parity_rows(wn, rows_n, got[name])
+        if "spec32k_tokens" in got.files:
+            parity["spec32k"] = _parity_verify(workloads.spec32k(), got["spec32k_tokens"], got["spec32k_nacc"])
     print(json.dumps({
         "value": len(sel) / med, "unit": "rows/s", "cores": 1, "kind": "port",
         "sample": f"{len(sel)} of {B} {workload} rows (evenly spaced, all parameter groups), "
@@ -128,15 +198,18 @@ def cpu_baseline_child(workload: str, rows: int, reps: int) -> None:
         "all_cores": {"value": len(sel) / pmed, "unit": "rows/s", "cores": n,
                       "sample": f"the same rows over {n} single-core processes, median of {reps} reps "
                                 f"of {pmed:.3f} s"},
+        "parity": parity,
     }))
 
 
-def run_cpu_baseline(workload: str, rows: int, reps: int):
+def run_cpu_baseline(workload: str, rows: int, reps: int, ids_path: str | None = None):
     env = dict(os.environ, OMP_NUM_THREADS="1", OPENBLAS_NUM_THREADS="1", MKL_NUM_THREADS="1",
                HIP_VISIBLE_DEVICES="", CUDA_VISIBLE_DEVICES="")
-    r = subprocess.run([sys.executable, str(Path(__file__).resolve()), "--cpu-baseline-child", "--workload", workload,
-                        "--cpu-rows", str(rows), "--cpu-reps", str(reps)],
-                       capture_output=True, text=True, env=env, timeout=900)
+    cmd = [sys.executable, str(Path(__file__).resolve()), "--cpu-baseline-child", "--workload", workload,
+           "--cpu-rows", str(rows), "--cpu-reps", str(reps)]
+    if ids_path:
+        cmd += ["--gpu-ids", ids_path]
+    r = subprocess.run(cmd, capture_output=True, text=True, env=env, timeout=900)
     if r.returncode != 0:
         sys.stderr.write(r.stderr)
         return None
@@ -218,9 +291,22 @@ def traffic_from(workload: str, fetch_dir: str, write_dir: str, dst: Path | None
     return out
 
 
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache
+ROTATE_BYTES = 2 * MALL_BYTES  # rotating input sets span at least this much, so steps stream from HBM
+
+
+def _n_sets(set_bytes: int, least: int = 2, most: int = 64) -> int:
+    """Copies to rotate: enough to span ROTATE_BYTES, at most `most` (a
+    config too small to fill the cache that way is latency-bound anyway and
+    is labelled cache-resident)."""
+    return min(most, max(least, -(-ROTATE_BYTES // max(1, set_bytes))))
+
+
 def bench_config(name: str, steps: int = 20, warmup: int = 3) -> dict:
-    """rows/s of one more sampling workload, inputs resident in HBM (two
-    rotating copies of the logits), timed with HIP events like the headline."""
+    """rows/s of one more sampling workload, inputs resident in HBM, timed
+    with HIP events like the headline.  Enough copies of the logits rotate
+    across steps to span twice the 256 MB Infinity Cache, so every step
+    reads its logits from HBM.  Also returns the ids of the last step."""
     import torch
 
     from pagellm_amd import _native, workloads
@@ -235,14 +321,16 @@ def bench_config(name: str, steps: int = 20, warmup: int = 3) -> dict:
     t, k, p, r = _pack_params(w["params"])
     hint = _nucleus_hint(t, k, p, w["logits"].shape[1])
     hist_ids, hist_off = _pack_histories(w["contexts"], w["params"], B, V)
-    xs = [torch.from_numpy(w["logits"]).to(dev) for _ in range(2)]
+    nsets = _n_sets(w["logits"].nbytes)
+    x0 = torch.from_numpy(w["logits"]).to(dev)
+    xs = [x0] + [x0.clone() for _ in range(nsets - 1)]
     d = {n: torch.from_numpy(a).to(dev) for n, a in
          dict(t=t, k=k, p=p, r=r, u=w["uniforms"], ids=hist_ids, off=hist_off).items() if a is not None}
     out = torch.empty(B, dtype=torch.int32, device=dev)
     torch.cuda.synchronize()
 
     def step(i):
-        ctx.sample(xs[i % 2].data_ptr(), _native.PLH_F32, V, B, V,
+        ctx.sample(xs[i % nsets].data_ptr(), _native.PLH_F32, V, B, V,
                    d["ids"].data_ptr() if "ids" in d else None, d["off"].data_ptr() if "off" in d else None,
                    d["t"].data_ptr(), d["k"].data_ptr(), d["p"].data_ptr(), d["r"].data_ptr(),
                    d["u"].data_ptr(), out.data_ptr(), None, hint)
@@ -262,16 +350,24 @@ def bench_config(name: str, steps: int = 20, warmup: int = 3) -> dict:
     nbytes = workloads.algorithmic_bytes(w)
     res = {"rows_per_s": B / (ms * 1e-3), "ms_per_step": ms, "batch": B, "vocab": V,
            "algorithmic_bytes_per_step": nbytes, "hbm_gbps": nbytes / (ms * 1e-3) / 1e9,
+           "rotating_input_sets": nsets, "inputs_bytes_rotated": nsets * w["logits"].nbytes,
+           "inputs_cache_resident": nsets * w["logits"].nbytes < MALL_BYTES,
            "fallback_rows_per_step": (ctx.fallback_rows() - fb0) / (warmup + steps)}
+    ids = out.cpu().numpy().astype("int64")
     ctx.close()
-    return res
+    del xs, x0
+    torch.cuda.empty_cache()
+    return res, ids
 
 
 def bench_verify(steps: int = 50, warmup: int = 5) -> dict:
     """The speculative verify workload (64 rows, k = 4, V = 32000, float64 p
     and q resident in HBM): rows/s and the data-dependent compulsory bytes
     (per row: 16 B per accept test, then the rows the final draw reads:
-    p and q of the rejected position, or p_k)."""
+    p and q of the rejected position, or p_k).  p/q copies rotate across
+    steps (each set is 147 MB; together they span twice the Infinity
+    Cache).  A second pass with the library's kernel timing gives the two
+    launches' average durations.  Also returns the last step's outputs."""
     import torch
 
     from pagellm_amd import _native, workloads
@@ -283,8 +379,11 @@ def bench_verify(steps: int = 50, warmup: int = 5) -> dict:
     stream = torch.cuda.Stream(device=dev)
     ctx = _native.Context(0)
     ctx.set_stream(stream.cuda_stream)
-    p = torch.from_numpy(w["p"]).to(dev)
-    q = torch.from_numpy(w["q"]).to(dev)
+    nsets = _n_sets(w["p"].nbytes + w["q"].nbytes)
+    p0 = torch.from_numpy(w["p"]).to(dev)
+    q0 = torch.from_numpy(w["q"]).to(dev)
+    ps = [p0] + [p0.clone() for _ in range(nsets - 1)]
+    qs = [q0] + [q0.clone() for _ in range(nsets - 1)]
     dr = torch.from_numpy(w["draft"].astype("int32")).to(dev)
     au = torch.from_numpy(w["accept_u"]).to(dev)
     ru = torch.from_numpy(w["resample_u"]).to(dev)
@@ -292,27 +391,38 @@ def bench_verify(steps: int = 50, warmup: int = 5) -> dict:
     nacc = torch.empty(B, dtype=torch.int32, device=dev)
     torch.cuda.synchronize()
 
-    def step():
-        ctx.verify(p.data_ptr(), q.data_ptr(), _native.PLH_F64, B, k, V, dr.data_ptr(), au.data_ptr(),
-                   ru.data_ptr(), False, tok.data_ptr(), nacc.data_ptr())
+    def step(i):
+        ctx.verify(ps[i % nsets].data_ptr(), qs[i % nsets].data_ptr(), _native.PLH_F64, B, k, V, dr.data_ptr(),
+                   au.data_ptr(), ru.data_ptr(), False, tok.data_ptr(), nacc.data_ptr())
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record(stream)
-    for _ in range(steps):
-        step()
-    b.record(stream)
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / steps
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            step(i)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for i in range(steps):
+            step(i)
+        b.record(stream)
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / steps
+        ctx.set_kernel_timing(True)
+        ctx.kernel_times()
+        for i in range(steps):
+            step(i)
+        parts_ms, draw_ms, calls = ctx.kernel_times()
+        ctx.set_kernel_timing(False)
     n = nacc.cpu().numpy()
     nbytes = int(sum(16 * (min(int(s) + 1, k)) + (16 * V if s < k else 8 * V) for s in n))
     res = {"rows_per_s": B / (ms * 1e-3), "ms_per_step": ms, "batch": B, "k": k, "vocab": V,
            "accepted_per_row": float(n.mean()), "compulsory_bytes_per_step": nbytes,
-           "hbm_gbps": nbytes / (ms * 1e-3) / 1e9}
+           "hbm_gbps": nbytes / (ms * 1e-3) / 1e9, "rotating_input_sets": nsets,
+           "kernel_ms": {"k_verify_parts": parts_ms / max(1, calls), "k_verify_draw": draw_ms / max(1, calls)}}
+    out = (tok.cpu().numpy().astype("int64"), n.astype("int64"))
     ctx.close()
-    return res
+    del ps, qs, p0, q0
+    torch.cuda.empty_cache()
+    return res, out
 
 
 def bench_head(steps: int = 20, warmup: int = 3, N: int = 256, D: int = 4096, V: int = 128256) -> dict:
@@ -431,6 +541,7 @@ def main() -> None:
     ap.add_argument("--cpu-rows", type=int, default=256)
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--cpu-baseline-child", action="store_true")
+    ap.add_argument("--gpu-ids", help="(child) .npz of the GPU ids each configuration produced")
     ap.add_argument("--pmc-probe", action="store_true", help="short run for rocprofv3 counter passes")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the other workloads (zipf32k, zipf152k, char65, spec32k verify)")
@@ -440,7 +551,7 @@ def main() -> None:
     args = ap.parse_args()
 
     if args.cpu_baseline_child:
-        cpu_baseline_child(args.workload, args.cpu_rows, args.cpu_reps)
+        cpu_baseline_child(args.workload, args.cpu_rows, args.cpu_reps, args.gpu_ids)
         return
     if args.traffic_from:
         traffic_from(args.workload, *args.traffic_from)
@@ -449,9 +560,14 @@ def main() -> None:
         pmc_probe(args.workload)
         return
     if args.only:
-        fns = {"spec32k": bench_verify, "head128k": bench_head}
-        fn = fns.get(args.only, lambda **kw: bench_config(args.only, **kw))
-        print(json.dumps(fn(steps=min(args.steps, 50), warmup=min(args.warmup, 5))), flush=True)
+        kw = dict(steps=min(args.steps, 50), warmup=min(args.warmup, 5))
+        if args.only == "head128k":
+            res = bench_head(**kw)
+        elif args.only == "spec32k":
+            res = bench_verify(**kw)[0]
+        else:
+            res = bench_config(args.only, **kw)[0]
+        print(json.dumps(res), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -537,17 +653,31 @@ def main() -> None:
     print("[bench] copy bandwidth", file=sys.stderr, flush=True)
     copy_gbps = copy_bandwidth()
     others = None
+    gpu_ids = {args.workload: ids.astype(np.int64)}
     if not args.no_other_configs:
         others = {}
         for name in ("char65", "zipf32k", "zipf152k"):
             if name != args.workload:
                 print(f"[bench] other config {name}", file=sys.stderr, flush=True)
-                others[name] = bench_config(name)
+                others[name], gpu_ids[name] = bench_config(name)
         print("[bench] other config spec32k (verify)", file=sys.stderr, flush=True)
-        others["spec32k"] = bench_verify()
+        others["spec32k"], (gpu_ids["spec32k_tokens"], gpu_ids["spec32k_nacc"]) = bench_verify()
         print("[bench] other config head128k (logits producer)", file=sys.stderr, flush=True)
         others["head128k"] = bench_head()
-    cpu = None if args.no_cpu_baseline else run_cpu_baseline(args.workload, args.cpu_rows, args.cpu_reps)
+    cpu = None
+    if not args.no_cpu_baseline:
+        import tempfile
+
+        print("[bench] CPU baseline and oracle parity", file=sys.stderr, flush=True)
+        with tempfile.TemporaryDirectory() as td:
+            ids_path = os.path.join(td, "gpu_ids.npz")
+            np.savez(ids_path, **gpu_ids)
+            cpu = run_cpu_baseline(args.workload, args.cpu_rows, args.cpu_reps, ids_path)
+    parity = cpu.pop("parity", None) if cpu else None
+    if others and parity:
+        for name, v in parity.items():
+            if name in others:
+                others[name]["parity"] = v
     res = {
         "metric": METRIC,
         "value": rows_per_s,
@@ -573,6 +703,7 @@ def main() -> None:
                      "frac": kernel_gbps / PEAK_HBM_GBPS if kernel_gbps else None,
                      "traffic": load_traffic(args.workload), "kernel": "k_sample_chunks",
                      "copy_gbps": copy_gbps, "frac_of_copy": kernel_gbps / copy_gbps if kernel_gbps else None},
+        "parity": parity.get(args.workload) if parity else None,
         "end_to_end": e2e,
         "cpu_baseline": cpu,
         "other_configs": others,

@@ -133,7 +133,9 @@ int plh_sample(plh_ctx* ctx, const void* logits, int dtype, int64_t ld, int B, i
 /*
  * apply_repetition_penalty() on a copy: src/pagellm/engine/sampling.py:52-62.
  * out[b, :V] = x[b, :V] with every distinct id of row b's history mapped
- * through x > 0 ? x / penalty : x * penalty, computed in `dtype`.
+ * through x > 0 ? x / penalty : x * penalty, computed in `dtype`.  `out`
+ * must not overlap `x` (PLH_ERR_INVALID_ARG): the penalty works on a copy,
+ * as the reference's does (:58).
  */
 int plh_penalize(plh_ctx* ctx, const void* x, int dtype, int64_t ld, int B, int V,
                  const int32_t* hist_ids, const int64_t* hist_off, const double* rep_penalty,
@@ -142,7 +144,8 @@ int plh_penalize(plh_ctx* ctx, const void* x, int dtype, int64_t ld, int B, int 
 /*
  * draw(): src/pagellm/engine/sampling.py:94-98 for B rows of non-negative
  * weights p[b, :V] (any scale): first i with cumsum(p)[i] > u[b] * sum(p),
- * else V-1.
+ * else V-1.  float32 rows are widened exactly and drawn in float64
+ * arithmetic (the reference's probs() hands draw() float64 rows).
  */
 int plh_draw(plh_ctx* ctx, const void* p, int dtype, int64_t ld, int B, int V,
              const double* uniforms, int32_t* out_ids);

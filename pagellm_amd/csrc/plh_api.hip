@@ -89,6 +89,26 @@ int reserve_ws(plh_ctx* c, size_t bytes) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// PLH_OPT_KERNEL_TIMING: takes an event triple (start, between, end) for
+// the call and records its start on the context's stream; the launch
+// records `between` after its first kernel and the caller `end` after the
+// last.  A no-op (null events) when timing is off.
+int timing_begin(plh_ctx* c, std::array<hipEvent_t, 3>& ev) {
+  if (!c->timing) return PLH_OK;
+  for (auto& e : ev) {
+    if (c->ev_free.empty()) {
+      hipEvent_t n = nullptr;
+      PLH_HIP(c, hipEventCreate(&n), "hipEventCreate");
+      c->ev_free.push_back(n);
+    }
+    e = c->ev_free.back();
+    c->ev_free.pop_back();
+  }
+  c->ev_pending.push_back(ev);
+  PLH_HIP(c, hipEventRecord(ev[0], c->stream), "hipEventRecord");
+  return PLH_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -320,19 +340,8 @@ int plh_sample(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, int
   if (rc != PLH_OK) return rc;
   a.ws = plh::fast_ws_layout(c->ws, B, V, f64);
   std::array<hipEvent_t, 3> ev{};
-  if (c->timing) {
-    for (auto& e : ev) {
-      if (c->ev_free.empty()) {
-        hipEvent_t n = nullptr;
-        PLH_HIP(c, hipEventCreate(&n), "hipEventCreate");
-        c->ev_free.push_back(n);
-      }
-      e = c->ev_free.back();
-      c->ev_free.pop_back();
-    }
-    c->ev_pending.push_back(ev);
-    PLH_HIP(c, hipEventRecord(ev[0], c->stream), "hipEventRecord");
-  }
+  rc = timing_begin(c, ev);
+  if (rc != PLH_OK) return rc;
   const hipError_t e = plh::launch_sample_fast(a, f64, vec, c->num_cu, c->stream, ev[1]);
   if (e != hipSuccess) return hip_fail(c, e, "plh_sample launch");
   if (c->timing) PLH_HIP(c, hipEventRecord(ev[2], c->stream), "hipEventRecord");
@@ -352,6 +361,16 @@ int plh_penalize(plh_ctx* c, const void* x, int dtype, int64_t ld, int B, int V,
     return fail(c, PLH_ERR_INVALID_ARG, "null device pointer%s");
   if (hist_off != nullptr && hist_ids == nullptr)
     return fail(c, PLH_ERR_INVALID_ARG, "hist_off given without hist_ids%s");
+  {
+    // the kernel copies x to out and then penalises out from x: in place, a
+    // repeated id could read a value another thread has already penalised
+    const size_t es = dtype == PLH_F64 ? 8 : 4;
+    const uintptr_t x0 = reinterpret_cast<uintptr_t>(x), o0 = reinterpret_cast<uintptr_t>(out);
+    const uintptr_t x1 = x0 + ((size_t)(B - 1) * (size_t)ld + (size_t)V) * es;
+    const uintptr_t o1 = o0 + ((size_t)(B - 1) * (size_t)out_ld + (size_t)V) * es;
+    if (x0 < o1 && o0 < x1)
+      return fail(c, PLH_ERR_INVALID_ARG, "out must not overlap x (the penalty works on a copy)%s");
+  }
   int rc = use_device(c);
   if (rc != PLH_OK) return rc;
   plh::PenalizeArgs a{x, ld, out, out_ld, B, V, hist_ids, hist_off, rep_penalty};
@@ -394,8 +413,12 @@ int plh_verify(plh_ctx* c, const void* p, const void* q, int dtype, int B, int k
   rc = reserve_ws(c, plh::verify_ws_bytes(B, V));
   if (rc != PLH_OK) return rc;
   const plh::VerifyWs ws = plh::verify_ws_layout(c->ws, B, V);
-  const hipError_t e = plh::launch_verify(a, ws, dtype == PLH_F64, c->stream);
+  std::array<hipEvent_t, 3> ev{};
+  rc = timing_begin(c, ev);
+  if (rc != PLH_OK) return rc;
+  const hipError_t e = plh::launch_verify(a, ws, dtype == PLH_F64, c->stream, ev[1]);
   if (e != hipSuccess) return hip_fail(c, e, "plh_verify launch");
+  if (c->timing) PLH_HIP(c, hipEventRecord(ev[2], c->stream), "hipEventRecord");
   PLH_HIP(c, hipEventRecord(c->ws_done, c->stream), "hipEventRecord");
   c->ws_stream = c->stream;
   return PLH_OK;

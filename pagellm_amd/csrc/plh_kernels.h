@@ -142,7 +142,9 @@ hipError_t launch_penalize(const PenalizeArgs& a, bool f64, hipStream_t s);
 // launches (stop positions and chunk sums, then the draw).
 size_t verify_ws_bytes(int B, int V);
 VerifyWs verify_ws_layout(void* base, int B, int V);
-hipError_t launch_verify(const VerifyArgs& a, const VerifyWs& ws, bool f64, hipStream_t s);
+// `between`, when not null, is recorded on s between the two launches.
+hipError_t launch_verify(const VerifyArgs& a, const VerifyWs& ws, bool f64, hipStream_t s,
+                         hipEvent_t between = nullptr);
 // Logits producer: workspace bytes (the normalised rows) and the two
 // launches (RMSNorm, then the MFMA product into out).
 size_t head_ws_bytes(int N, int D);

@@ -260,16 +260,20 @@ VerifyWs verify_ws_layout(void* base, int B, int V) {
 }
 
 template <typename TIn>
-hipError_t launch_verify_t(const VerifyArgs& a, const VerifyWs& ws, hipStream_t s) {
+hipError_t launch_verify_t(const VerifyArgs& a, const VerifyWs& ws, hipStream_t s, hipEvent_t between) {
   const dim3 block(kThreads);
   const dim3 grid_parts((unsigned)((size_t)a.B * ws.C));
   hipLaunchKernelGGL((k_verify_parts<TIn>), grid_parts, block, 0, s, a, ws);
+  if (between != nullptr) {
+    const hipError_t e = hipEventRecord(between, s);
+    if (e != hipSuccess) return e;
+  }
   hipLaunchKernelGGL((k_verify_draw<TIn>), dim3(a.B), block, 0, s, a, ws);
   return hipGetLastError();
 }
 
-hipError_t launch_verify(const VerifyArgs& a, const VerifyWs& ws, bool f64, hipStream_t s) {
-  return f64 ? launch_verify_t<double>(a, ws, s) : launch_verify_t<float>(a, ws, s);
+hipError_t launch_verify(const VerifyArgs& a, const VerifyWs& ws, bool f64, hipStream_t s, hipEvent_t between) {
+  return f64 ? launch_verify_t<double>(a, ws, s, between) : launch_verify_t<float>(a, ws, s, between);
 }
 
 }  // namespace plh

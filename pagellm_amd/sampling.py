@@ -26,8 +26,10 @@ from .params import SamplingParams, make_rng
 
 __all__ = [
     "SamplingParams",
+    "abi_params",
     "apply_repetition_penalty",
     "draw",
+    "draw_batch",
     "make_rng",
     "probs",
     "sample",
@@ -62,6 +64,9 @@ def _history_ids(context, V: int) -> np.ndarray:
     return ids.astype(np.int32)
 
 
+MAX_PENALTY_VOCAB = 262144  # vocabulary size up to which penalised rows are supported
+
+
 def _pack_histories(contexts, params: Sequence[SamplingParams], B: int, V: int):
     """CSR (ids, offsets) of the histories of rows whose penalty is active,
     or (None, None) when no row needs one (nothing is uploaded)."""
@@ -80,6 +85,12 @@ def _pack_histories(contexts, params: Sequence[SamplingParams], B: int, V: int):
         off[b + 1] = off[b] + n
     if off[-1] == 0:
         return None, None
+    if V > MAX_PENALTY_VOCAB:
+        raise NotImplementedError(
+            f"repetition penalty over a token history needs V <= {MAX_PENALTY_VOCAB} here (got V = {V}): "
+            "the kernels mark a row's penalised tokens in an on-chip bitmap of that many bits; "
+            "the reference (sampling.py:52-62) has no such limit"
+        )
     return np.concatenate(parts), off
 
 
@@ -105,6 +116,24 @@ def _pack_params(params: Sequence[SamplingParams]):
     if idx is None:
         return t, k, p, r
     return t[idx], k[idx], p[idx], r[idx]
+
+
+def abi_params(params: Sequence) -> dict[str, np.ndarray]:
+    """The per-row parameter arrays ``plh_sample`` reads for one batch:
+    ``temperature``, ``top_p``, ``repetition_penalty`` float64 [B] and
+    ``top_k`` int32 [B] (clamped to 2^31 - 1, which disables the mask as any
+    top_k >= V does).
+
+    Each entry is a ``SamplingParams``, or a parsed request that carries one
+    in ``.params`` (the reference's ``CompletionRequest``,
+    ``src/pagellm/serving/protocol.py:75-79``, as its
+    ``parse_completion_request`` returns it, ``:82-108``).  A JSON number
+    parses to a Python float, an IEEE double, so every value reaches the
+    kernels bit for bit.  This is the packing every sampler entry point uses.
+    """
+    rows = [r if hasattr(r, "temperature") else r.params for r in params]
+    t, k, p, r = _pack_params(rows)
+    return {"temperature": t, "top_k": k, "top_p": p, "repetition_penalty": r}
 
 
 def _expand_params(params, B: int) -> list[SamplingParams]:
@@ -273,6 +302,30 @@ def draw(p: np.ndarray, rng: np.random.Generator) -> int:
     d_o = c.scratch("draw_out", (1,), np.int32)
     c.draw(d_p.ptr, _native.dtype_code(x.dtype), V, 1, V, d_u.ptr, d_o.ptr)
     return int(d_o.download()[0])
+
+
+def draw_batch(p, uniforms, *, ctx: _native.Context | None = None) -> np.ndarray:
+    """Batched :func:`draw` with explicit uniforms: row b of ``p [B, V]`` is
+    drawn at ``uniforms[b]`` (``sampling.py:94-98``: the first index whose
+    running mass exceeds ``u * total``, clamped to V - 1).  A float32 ``p`` is
+    widened exactly and drawn in float64 arithmetic (the reference's
+    ``probs()`` always hands ``draw`` float64 rows).  Returns int64 ids [B]."""
+    x = _as_float_rows(p)
+    if x.ndim != 2 or x.shape[1] == 0:
+        raise ValueError("p must be a 2-D array with at least one column")
+    u = np.ascontiguousarray(uniforms, dtype=np.float64).reshape(-1)
+    B, V = x.shape
+    if u.shape[0] != B:
+        raise ValueError(f"expected {B} uniforms, got {u.shape[0]}")
+    if B == 0:
+        return np.zeros(0, dtype=np.int64)
+    c = _ctx(ctx)
+    c.set_stream(None)
+    d_p = c.scratch_upload("drawb_p", x)
+    d_u = c.scratch_upload("drawb_u", u)
+    d_o = c.scratch("drawb_out", (B,), np.int32)
+    c.draw(d_p.ptr, _native.dtype_code(x.dtype), V, B, V, d_u.ptr, d_o.ptr)
+    return d_o.download().astype(np.int64)
 
 
 def sample(logits: np.ndarray, params: SamplingParams, rng: np.random.Generator, context=()) -> int:

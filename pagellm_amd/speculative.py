@@ -95,10 +95,20 @@ def verify(p_rows: np.ndarray, q_rows: np.ndarray, draft_tokens, rng) -> tuple[l
     return out, s
 
 
-def verify_batch(p, q, draft, accept_u, resample_u, *, ctx: _native.Context | None = None):
-    """Batched verify with explicit uniforms: test i of row b uses
-    ``accept_u[b, i]``; the emitted (residual or bonus) token of row b uses
-    ``resample_u[b]``.  p [B,k+1,V], q [B,k,V], draft [B,k].
+def verify_batch(p, q, draft, accept_u, resample_u=None, *, ctx: _native.Context | None = None):
+    """Batched verify.  p [B,k+1,V], q [B,k,V], draft [B,k].
+
+    Two forms of randomness:
+
+    * ``verify_batch(p, q, draft, rngs)``: ``rngs[b]`` is row b's Generator,
+      consumed exactly as the reference's ``verify`` consumes it
+      (``speculative.py:50``, ``:57``, ``:59``): one ``random()`` per accept
+      test up to the first rejection, then one for the emitted token.  Each
+      Generator is left where the reference leaves it.
+    * ``verify_batch(p, q, draft, accept_u, resample_u)``: explicit uniforms,
+      test i of row b uses ``accept_u[b, i]`` and the emitted (residual or
+      bonus) token ``resample_u[b]``.
+
     Returns (tokens int64 [B,k+1] padded with -1, n_acc int64 [B])."""
     c = ctx if ctx is not None else _native.default_context()
     p = _as_float_rows(p)
@@ -110,6 +120,23 @@ def verify_batch(p, q, draft, accept_u, resample_u, *, ctx: _native.Context | No
     if q.shape != (B, k, V):
         raise ValueError(f"q must be {(B, k, V)}, got {q.shape}")
     d = _check_draft(np.asarray(draft).reshape(B, k), V)
+    if resample_u is None:
+        rngs = list(accept_u)
+        if len(rngs) != B:
+            raise ValueError(f"expected {B} Generators, got {len(rngs)}")
+        # per row: k + 1 uniforms drawn ahead (u_0..u_{k-1} for the tests;
+        # the draw at stop s uses u_{s+1}, or u_k after k acceptances), then
+        # each Generator replayed to the count the reference consumes
+        states = [g.bit_generator.state for g in rngs]
+        u = np.array([[g.random() for _ in range(k + 1)] for g in rngs], dtype=np.float64).reshape(B, k + 1)
+        a = np.ascontiguousarray(u[:, :k])
+        w = np.ascontiguousarray(u[:, np.minimum(np.arange(k + 1) + 1, k)])
+        toks, n = _run(c, p, q, d, a, w, True)
+        for g, st, s in zip(rngs, states, n):
+            g.bit_generator.state = st
+            for _ in range(int(s) + 2 if s < k else k + 1):
+                g.random()
+        return toks.astype(np.int64), n.astype(np.int64)
     a = np.ascontiguousarray(accept_u, dtype=np.float64).reshape(B, k)
     w = np.ascontiguousarray(resample_u, dtype=np.float64).reshape(B)
     toks, n = _run(c, p, q, d, a, w, False)

@@ -167,3 +167,28 @@ def test_nucleus_hint_changes_the_path_not_the_ids():
     for b in range(B):
         ref = oracle.sample(x[b], params[b], u[b], hists[b])
         assert hinted[b] == ref or min(oracle.sampler.sample_boundary_gaps(x[b], params[b], u[b], hists[b])) < 1e-6
+
+
+def test_penalize_rejects_in_place_and_overlapping_output():
+    """plh_penalize works on a copy (sampling.py:58): an output that overlaps
+    the input is an invalid argument, and a disjoint one is penalised once
+    per distinct id even when the history repeats ids."""
+    c = _native.default_context()
+    V, B = 1000, 2
+    g = np.random.default_rng(8)
+    x = g.normal(0, 2, (B, V)).astype(np.float32)
+    ids = np.array([5, 5, 5, 7, 999, 5, 7], dtype=np.int32)
+    off = np.array([0, 7, 7], dtype=np.int64)
+    pen = np.array([1.5, 1.5])
+    d_x = c.to_device(x)
+    d_ids, d_off, d_pen = c.to_device(ids), c.to_device(off), c.to_device(pen)
+    with pytest.raises(ValueError, match="overlap"):
+        c.penalize(d_x.ptr, _native.PLH_F32, V, B, V, d_ids.ptr, d_off.ptr, d_pen.ptr, d_x.ptr, V)
+    with pytest.raises(ValueError, match="overlap"):  # shifted by one element into row 0
+        c.penalize(d_x.ptr, _native.PLH_F32, V, B, V, d_ids.ptr, d_off.ptr, d_pen.ptr, d_x.ptr + 4, V)
+    d_o = c.empty((B, V), np.float32)
+    c.penalize(d_x.ptr, _native.PLH_F32, V, B, V, d_ids.ptr, d_off.ptr, d_pen.ptr, d_o.ptr, V)
+    got = d_o.download()
+    assert np.array_equal(got[0], oracle.apply_repetition_penalty(x[0], ids.tolist(), 1.5))
+    assert np.array_equal(got[1], x[1])
+    assert np.array_equal(d_x.download(), x)  # the input is untouched

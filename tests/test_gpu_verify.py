@@ -70,6 +70,27 @@ def test_verify_replays_generator_exactly():
         assert a.random() == b.random()
 
 
+def test_verify_batch_generator_form_matches_the_reference_loop():
+    """verify_batch(p, q, draft, rngs): each row's Generator is consumed as
+    the reference's verify consumes it (one draw per accept test up to the
+    first rejection, one for the emitted token), so the outputs equal the
+    oracle's per-row loop on identical Generators and every Generator ends in
+    the same state; k = 0 included."""
+    g = np.random.default_rng(12)
+    for trial, (B, k, V) in enumerate([(16, 4, 40), (9, 0, 17), (33, 2, 5), (8, 6, 3000)]):
+        p = np.stack([[_dist(g, V, 1.5) for _ in range(k + 1)] for _ in range(B)])
+        q = np.array([[_dist(g, V, 1.5) for _ in range(k)] for _ in range(B)]).reshape(B, k, V)
+        draft = np.array([[int(g.choice(V, p=q[b, i])) for i in range(k)] for b in range(B)]).reshape(B, k)
+        mine = [np.random.default_rng([trial, b]) for b in range(B)]
+        ref = [np.random.default_rng([trial, b]) for b in range(B)]
+        toks, n = verify_batch(p, q, draft, mine)
+        for b in range(B):
+            out, acc = oracle.verify(p[b], q[b], [int(t) for t in draft[b]], ref[b])
+            assert int(n[b]) == acc and [int(t) for t in toks[b, : acc + 1]] == out, (trial, b)
+            assert (toks[b, acc + 1 :] == -1).all()
+            assert mine[b].random() == ref[b].random(), (trial, b)
+
+
 def test_spec32k_parity():
     w = workloads.spec32k()
     toks, n = verify_batch(w["p"], w["q"], w["draft"], w["accept_u"], w["resample_u"])

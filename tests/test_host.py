@@ -137,3 +137,19 @@ def test_nucleus_hint_only_for_high_top_p_rows_without_top_k():
     assert hint([SamplingParams(top_p=0.99, top_k=40)]) == 0
     assert hint([SamplingParams(top_p=0.99, temperature=0.0)]) == 0
     assert hint([SamplingParams(), SamplingParams(top_p=0.995)]) == _native.PLH_SAMPLE_NUCLEUS
+
+
+def test_penalised_rows_beyond_the_bitmap_fail_on_the_host_with_the_reason():
+    """Penalised histories need V <= 262144 (the kernels' per-row bitmap);
+    a larger vocabulary is refused before anything reaches the device, with
+    the reason.  Rows without an active penalty are not affected."""
+    from pagellm_amd.sampling import MAX_PENALTY_VOCAB, _pack_histories
+
+    V = MAX_PENALTY_VOCAB + 1
+    pen, plain = SamplingParams(repetition_penalty=1.1), SamplingParams()
+    with pytest.raises(NotImplementedError, match="262144"):
+        _pack_histories([[1, 2, 3]], [pen], 1, V)
+    assert _pack_histories([[1, 2, 3]], [plain], 1, V) == (None, None)
+    assert _pack_histories([[]], [pen], 1, V) == (None, None)
+    ids, off = _pack_histories([[1, 2, 3]], [pen], 1, MAX_PENALTY_VOCAB)
+    assert list(ids) == [1, 2, 3] and list(off) == [0, 3]
