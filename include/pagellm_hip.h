@@ -131,6 +131,23 @@ int plh_sample(plh_ctx* ctx, const void* logits, int dtype, int64_t ld, int B, i
                const double* uniforms, int32_t* out_ids, double* out_probs, int flags);
 
 /*
+ * plh_sample without any allocation.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory during the call (code
+ * under HIP graph capture, serving loops that forbid hipMalloc).  Same
+ * arguments, kernels and results as plh_sample; the fast path's workspace
+ * is a fixed 64 MiB array per GPU (a static device array, resolved when the
+ * context is created), never the context's growable workspace, and the
+ * kernel-timing option is ignored.  A batch whose workspace exceeds 64 MiB
+ * returns PLH_ERR_INVALID_ARG (mixed128k, 256 x 128256 fp32, fits).  Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (two streams, two contexts) race.
+ */
+int plh_sample_noalloc(plh_ctx* ctx, const void* logits, int dtype, int64_t ld, int B, int V,
+                       const int32_t* hist_ids, const int64_t* hist_off, const double* temperature,
+                       const int32_t* top_k, const double* top_p, const double* rep_penalty,
+                       const double* uniforms, int32_t* out_ids, double* out_probs, int flags);
+
+/*
  * apply_repetition_penalty() on a copy: src/pagellm/engine/sampling.py:52-62.
  * out[b, :V] = x[b, :V] with every distinct id of row b's history mapped
  * through x > 0 ? x / penalty : x * penalty, computed in `dtype`.  `out`

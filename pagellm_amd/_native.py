@@ -54,6 +54,10 @@ SIGNATURES = {
         _c_int,
         [_vp, _vp, _c_int, _c_i64, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int],
     ),
+    "plh_sample_noalloc": (
+        _c_int,
+        [_vp, _vp, _c_int, _c_i64, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int],
+    ),
     "plh_penalize": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_int, _c_int, _vp, _vp, _vp, _vp, _c_i64]),
     "plh_draw": (_c_int, [_vp, _vp, _c_int, _c_i64, _c_int, _c_int, _vp, _vp]),
     "plh_verify": (
@@ -295,6 +299,17 @@ class Context:
                rep_penalty, uniforms, out_ids, out_probs=None, flags=0) -> None:
         self._check(
             self.lib.plh_sample(
+                self.handle, logits_ptr, dtype_code, ld, B, V, hist_ids, hist_off, temperature, top_k, top_p,
+                rep_penalty, uniforms, out_ids, out_probs, flags,
+            )
+        )
+
+    def sample_noalloc(self, logits_ptr, dtype_code, ld, B, V, hist_ids, hist_off, temperature, top_k, top_p,
+                       rep_penalty, uniforms, out_ids, out_probs=None, flags=0) -> None:
+        """plh_sample_noalloc: plh_sample with the fast path's workspace in the
+        library's fixed per-GPU scratch array (no allocation during the call)."""
+        self._check(
+            self.lib.plh_sample_noalloc(
                 self.handle, logits_ptr, dtype_code, ld, B, V, hist_ids, hist_off, temperature, top_k, top_p,
                 rep_penalty, uniforms, out_ids, out_probs, flags,
             )

@@ -4,6 +4,7 @@
 #include <string.h>
 
 #include <array>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -25,6 +26,8 @@ struct plh_ctx {
   size_t ws_bytes = 0;
   hipEvent_t ws_done = nullptr;
   hipStream_t ws_stream = nullptr;
+  // plh_sample_noalloc: this device's copy of the file-scope scratch array
+  void* scratch = nullptr;
   // PLH_OPT_KERNEL_TIMING: event triples (start, between, end) per timed call
   bool timing = false;
   std::vector<hipEvent_t> ev_free;
@@ -109,6 +112,113 @@ int timing_begin(plh_ctx* c, std::array<hipEvent_t, 3>& ev) {
   return PLH_OK;
 }
 
+constexpr size_t kScratchBytes = size_t(64) << 20;  // the no-allocation entry point's workspace, per GPU
+constexpr int kMaxDevices = 64;
+
+}  // namespace
+
+// Workspace of plh_sample_noalloc: one copy per GPU the library runs on,
+// held until the process ends, zeroed when the code object loads.  In host
+// code `scratch` names a host-side stand-in, never the device memory: host
+// code uses only the address hipGetSymbolAddress returns for the current
+// device (resolve_scratch).
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Called by plh_create with the context's device current: the device
+// address of this device's scratch array, looked up once per device.
+int resolve_scratch(plh_ctx* c) {
+  if (c->device >= kMaxDevices) return fail(c, PLH_ERR_UNSUPPORTED, "device ordinal above 63%s");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[c->device] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) return hip_fail(c, e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[c->device] = p;
+  }
+  c->scratch = g_scratch_ptr[c->device];
+  return PLH_OK;
+}
+
+// plh_sample and plh_sample_noalloc: the same validation and kernels; the
+// fast path's workspace is the context's (grown on demand) or, with
+// noalloc, this device's scratch array (no allocation of any kind: no
+// workspace growth, no timing events).
+int sample_impl(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, int V, const int32_t* hist_ids,
+                const int64_t* hist_off, const double* temperature, const int32_t* top_k, const double* top_p,
+                const double* rep_penalty, const double* uniforms, int32_t* out_ids, double* out_probs, int flags,
+                bool noalloc) {
+  if (c == nullptr) return PLH_ERR_INVALID_ARG;
+  if (B < 0 || V < 1) return fail(c, PLH_ERR_INVALID_ARG, "need B >= 0 and V >= 1%s");
+  if (B == 0) return PLH_OK;
+  if (dtype != PLH_F32 && dtype != PLH_F64) return fail(c, PLH_ERR_INVALID_ARG, "dtype must be PLH_F32 or PLH_F64%s");
+  if (ld < V) return fail(c, PLH_ERR_INVALID_ARG, "ld must be >= V%s");
+  if (logits == nullptr || temperature == nullptr || top_k == nullptr || top_p == nullptr ||
+      rep_penalty == nullptr || out_ids == nullptr)
+    return fail(c, PLH_ERR_INVALID_ARG, "null device pointer%s");
+  if (hist_off != nullptr && hist_ids == nullptr)
+    return fail(c, PLH_ERR_INVALID_ARG, "hist_off given without hist_ids%s");
+  if (hist_off != nullptr && V > kMaxVBitmap)
+    return fail(c, PLH_ERR_UNSUPPORTED, "repetition-penalty histories need V <= 262144%s");
+  int rc = use_device(c);
+  if (rc != PLH_OK) return rc;
+  const size_t esize = dtype == PLH_F64 ? 8 : 4;
+  const bool vec = aligned16(logits) && ((size_t)ld * esize) % 16 == 0;
+  plh::SampleArgs a{};
+  a.logits = logits;
+  a.ld = ld;
+  a.B = B;
+  a.V = V;
+  a.hist_ids = hist_ids;
+  a.hist_off = hist_off;
+  a.hist_spans = (flags & PLH_SAMPLE_HIST_SPANS) ? 1 : 0;
+  a.temperature = temperature;
+  a.top_k = top_k;
+  a.top_p = top_p;
+  a.rep_penalty = rep_penalty;
+  a.uniforms = uniforms;
+  a.out_ids = out_ids;
+  a.out_probs = out_probs;
+  a.fallback_rows = c->fallback;
+  a.nucleus = (flags & PLH_SAMPLE_NUCLEUS) ? 1 : 0;
+  const bool f64 = dtype == PLH_F64;
+  // the fast path gathers per-row state in LDS sized for V <= 262144
+  if (out_probs != nullptr || (flags & PLH_SAMPLE_ROWWISE) || V > kMaxVBitmap) {
+    const hipError_t e = plh::launch_sample_rows(a, f64, vec, c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "plh_sample launch");
+    return PLH_OK;
+  }
+  const size_t need = plh::fast_ws_bytes(B, V, f64);
+  if (noalloc) {
+    if (need > kScratchBytes) {
+      char msg[160];
+      snprintf(msg, sizeof(msg), "this batch needs %zu bytes of workspace; plh_sample_noalloc holds %zu%%s", need,
+               kScratchBytes);
+      return fail(c, PLH_ERR_INVALID_ARG, msg);
+    }
+    a.ws = plh::fast_ws_layout(c->scratch, B, V, f64);
+    const hipError_t e = plh::launch_sample_fast(a, f64, vec, c->num_cu, c->stream, nullptr);
+    if (e != hipSuccess) return hip_fail(c, e, "plh_sample_noalloc launch");
+    return PLH_OK;
+  }
+  rc = reserve_ws(c, need);
+  if (rc != PLH_OK) return rc;
+  a.ws = plh::fast_ws_layout(c->ws, B, V, f64);
+  std::array<hipEvent_t, 3> ev{};
+  rc = timing_begin(c, ev);
+  if (rc != PLH_OK) return rc;
+  const hipError_t e = plh::launch_sample_fast(a, f64, vec, c->num_cu, c->stream, ev[1]);
+  if (e != hipSuccess) return hip_fail(c, e, "plh_sample launch");
+  if (c->timing) PLH_HIP(c, hipEventRecord(ev[2], c->stream), "hipEventRecord");
+  PLH_HIP(c, hipEventRecord(c->ws_done, c->stream), "hipEventRecord");
+  c->ws_stream = c->stream;
+  return PLH_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -134,6 +244,7 @@ int plh_create(plh_ctx** out, int device) {
     if (hipEventCreateWithFlags(&c->ws_done, hipEventDisableTiming) != hipSuccess) { rc = PLH_ERR_HIP; break; }
     if (hipDeviceGetAttribute(&c->num_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
         c->num_cu <= 0) { rc = PLH_ERR_HIP; break; }
+    rc = resolve_scratch(c);
   } while (0);
   if (rc != PLH_OK) {
     plh_destroy(c);
@@ -296,58 +407,16 @@ int plh_sample(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, int
                const int64_t* hist_off, const double* temperature, const int32_t* top_k, const double* top_p,
                const double* rep_penalty, const double* uniforms, int32_t* out_ids, double* out_probs,
                int flags) {
-  if (c == nullptr) return PLH_ERR_INVALID_ARG;
-  if (B < 0 || V < 1) return fail(c, PLH_ERR_INVALID_ARG, "need B >= 0 and V >= 1%s");
-  if (B == 0) return PLH_OK;
-  if (dtype != PLH_F32 && dtype != PLH_F64) return fail(c, PLH_ERR_INVALID_ARG, "dtype must be PLH_F32 or PLH_F64%s");
-  if (ld < V) return fail(c, PLH_ERR_INVALID_ARG, "ld must be >= V%s");
-  if (logits == nullptr || temperature == nullptr || top_k == nullptr || top_p == nullptr ||
-      rep_penalty == nullptr || out_ids == nullptr)
-    return fail(c, PLH_ERR_INVALID_ARG, "null device pointer%s");
-  if (hist_off != nullptr && hist_ids == nullptr)
-    return fail(c, PLH_ERR_INVALID_ARG, "hist_off given without hist_ids%s");
-  if (hist_off != nullptr && V > kMaxVBitmap)
-    return fail(c, PLH_ERR_UNSUPPORTED, "repetition-penalty histories need V <= 262144%s");
-  int rc = use_device(c);
-  if (rc != PLH_OK) return rc;
-  const size_t esize = dtype == PLH_F64 ? 8 : 4;
-  const bool vec = aligned16(logits) && ((size_t)ld * esize) % 16 == 0;
-  plh::SampleArgs a{};
-  a.logits = logits;
-  a.ld = ld;
-  a.B = B;
-  a.V = V;
-  a.hist_ids = hist_ids;
-  a.hist_off = hist_off;
-  a.hist_spans = (flags & PLH_SAMPLE_HIST_SPANS) ? 1 : 0;
-  a.temperature = temperature;
-  a.top_k = top_k;
-  a.top_p = top_p;
-  a.rep_penalty = rep_penalty;
-  a.uniforms = uniforms;
-  a.out_ids = out_ids;
-  a.out_probs = out_probs;
-  a.fallback_rows = c->fallback;
-  a.nucleus = (flags & PLH_SAMPLE_NUCLEUS) ? 1 : 0;
-  const bool f64 = dtype == PLH_F64;
-  // the fast path gathers per-row state in LDS sized for V <= 262144
-  if (out_probs != nullptr || (flags & PLH_SAMPLE_ROWWISE) || V > kMaxVBitmap) {
-    const hipError_t e = plh::launch_sample_rows(a, f64, vec, c->stream);
-    if (e != hipSuccess) return hip_fail(c, e, "plh_sample launch");
-    return PLH_OK;
-  }
-  rc = reserve_ws(c, plh::fast_ws_bytes(B, V, f64));
-  if (rc != PLH_OK) return rc;
-  a.ws = plh::fast_ws_layout(c->ws, B, V, f64);
-  std::array<hipEvent_t, 3> ev{};
-  rc = timing_begin(c, ev);
-  if (rc != PLH_OK) return rc;
-  const hipError_t e = plh::launch_sample_fast(a, f64, vec, c->num_cu, c->stream, ev[1]);
-  if (e != hipSuccess) return hip_fail(c, e, "plh_sample launch");
-  if (c->timing) PLH_HIP(c, hipEventRecord(ev[2], c->stream), "hipEventRecord");
-  PLH_HIP(c, hipEventRecord(c->ws_done, c->stream), "hipEventRecord");
-  c->ws_stream = c->stream;
-  return PLH_OK;
+  return sample_impl(c, logits, dtype, ld, B, V, hist_ids, hist_off, temperature, top_k, top_p, rep_penalty,
+                     uniforms, out_ids, out_probs, flags, false);
+}
+
+int plh_sample_noalloc(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, int V,
+                       const int32_t* hist_ids, const int64_t* hist_off, const double* temperature,
+                       const int32_t* top_k, const double* top_p, const double* rep_penalty,
+                       const double* uniforms, int32_t* out_ids, double* out_probs, int flags) {
+  return sample_impl(c, logits, dtype, ld, B, V, hist_ids, hist_off, temperature, top_k, top_p, rep_penalty,
+                     uniforms, out_ids, out_probs, flags, true);
 }
 
 int plh_penalize(plh_ctx* c, const void* x, int dtype, int64_t ld, int B, int V, const int32_t* hist_ids,
