@@ -30,10 +30,7 @@ struct plh_ctx {
   hipStream_t ws_stream = nullptr;
   // plh_sample_noalloc: this device's copy of the file-scope scratch array
   void* scratch = nullptr;
-  // one-launch fast path: per-wave records, zeroed whenever (re)allocated
-  void* rec = nullptr;
-  size_t rec_bytes = 0;
-  bool stream_path = false;  // PLH_STREAM_PATH=1: the one-launch streaming kernel
+  bool stream_path = false;  // PLH_STREAM_PATH=1: the streaming kernels
   // PLH_OPT_KERNEL_TIMING: event triples (start, between, end) per timed call
   bool timing = false;
   std::vector<hipEvent_t> ev_free;
@@ -96,29 +93,6 @@ int reserve_ws(plh_ctx* c, size_t bytes) {
   return PLH_OK;
 }
 
-// The one-launch fast path's record region: grown like the workspace and
-// zeroed when (re)allocated, so a record slot only ever holds a tag of an
-// earlier call (tags are never zero).
-int reserve_rec(plh_ctx* c, size_t bytes) {
-  if (bytes <= c->rec_bytes) return PLH_OK;
-  if (c->ws_stream != nullptr) PLH_HIP(c, hipStreamSynchronize(c->ws_stream), "hipStreamSynchronize");
-  if (c->rec != nullptr) {
-    PLH_HIP(c, hipFree(c->rec), "hipFree");
-    c->rec = nullptr;
-    c->rec_bytes = 0;
-  }
-  const size_t sz = align_up(bytes + bytes / 4, 1u << 20);
-  PLH_HIP(c, hipMalloc(&c->rec, sz), "hipMalloc(records)");
-  PLH_HIP(c, hipMemsetAsync(c->rec, 0, sz, c->stream), "hipMemsetAsync(records)");
-  c->rec_bytes = sz;
-  return PLH_OK;
-}
-
-// Tag of one fast-path call: unique in the process (bit 30 set, so never
-// zero and never a token id or a zeroed word).
-std::atomic<uint32_t> g_call_gen{0};
-uint32_t next_gen() { return ((g_call_gen.fetch_add(1) + 1) & 0x3fffffffu) | 0x40000000u; }
-
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // PLH_OPT_KERNEL_TIMING: takes an event triple (start, between, end) for
@@ -142,7 +116,6 @@ int timing_begin(plh_ctx* c, std::array<hipEvent_t, 3>& ev) {
 }
 
 constexpr size_t kScratchBytes = size_t(64) << 20;  // the no-allocation entry point's workspace, per GPU
-constexpr size_t kScratchRec = size_t(8) << 20;     // of which the record region (zero at load)
 constexpr int kMaxDevices = 64;
 
 }  // namespace
@@ -246,38 +219,28 @@ int sample_impl(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, in
     c->ws_stream = c->stream;
     return PLH_OK;
   }
-  const size_t need_rec = plh::stream_rec_bytes(B, V, f64);
   const size_t need = plh::stream_ws_bytes(B, V, f64);
   if (noalloc) {
-    if (need_rec > kScratchRec || need > kScratchBytes - kScratchRec) {
+    if (need > kScratchBytes) {
       char msg[200];
-      snprintf(msg, sizeof(msg),
-               "this batch needs %zu + %zu bytes of workspace; plh_sample_noalloc holds %zu + %zu%%s", need_rec, need,
-               kScratchRec, kScratchBytes - kScratchRec);
+      snprintf(msg, sizeof(msg), "this batch needs %zu bytes of workspace; plh_sample_noalloc holds %zu%%s", need,
+               kScratchBytes);
       return fail(c, PLH_ERR_INVALID_ARG, msg);
     }
-    char* base = static_cast<char*>(c->scratch);
-    a.sw = plh::stream_ws_layout(base, base + kScratchRec, B, V, f64);
-    a.sw.gen = next_gen();
-    const hipError_t e = plh::launch_sample_stream(a, f64, vec, c->stream);
+    a.sw = plh::stream_ws_layout(c->scratch, B, V, f64);
+    const hipError_t e = plh::launch_sample_stream(a, f64, vec, c->stream, nullptr);
     if (e != hipSuccess) return hip_fail(c, e, "plh_sample_noalloc launch");
     return PLH_OK;
   }
   rc = reserve_ws(c, need);
   if (rc != PLH_OK) return rc;
-  rc = reserve_rec(c, need_rec);
-  if (rc != PLH_OK) return rc;
-  a.sw = plh::stream_ws_layout(c->rec, c->ws, B, V, f64);
-  a.sw.gen = next_gen();
+  a.sw = plh::stream_ws_layout(c->ws, B, V, f64);
   std::array<hipEvent_t, 3> ev{};
   rc = timing_begin(c, ev);
   if (rc != PLH_OK) return rc;
-  const hipError_t e = plh::launch_sample_stream(a, f64, vec, c->stream);
+  const hipError_t e = plh::launch_sample_stream(a, f64, vec, c->stream, ev[1]);
   if (e != hipSuccess) return hip_fail(c, e, "plh_sample launch");
-  if (c->timing) {  // one launch: the whole kernel counts as streaming time
-    PLH_HIP(c, hipEventRecord(ev[1], c->stream), "hipEventRecord");
-    PLH_HIP(c, hipEventRecord(ev[2], c->stream), "hipEventRecord");
-  }
+  if (c->timing) PLH_HIP(c, hipEventRecord(ev[2], c->stream), "hipEventRecord");
   PLH_HIP(c, hipEventRecord(c->ws_done, c->stream), "hipEventRecord");
   c->ws_stream = c->stream;
   return PLH_OK;
@@ -326,7 +289,6 @@ void plh_destroy(plh_ctx* c) {
   if (c->stream != nullptr) (void)hipStreamSynchronize(c->stream);
   if (c->ws_stream != nullptr) (void)hipStreamSynchronize(c->ws_stream);
   if (c->ws != nullptr) (void)hipFree(c->ws);
-  if (c->rec != nullptr) (void)hipFree(c->rec);
   if (c->ws_done != nullptr) (void)hipEventDestroy(c->ws_done);
   for (auto& t : c->ev_pending)
     for (hipEvent_t e : t) c->ev_free.push_back(e);

@@ -56,8 +56,8 @@ struct ChunkWs {
   int capc;         // candidate slots per chunk
 };
 
-// One-launch fast path (plh_stream.hip): the record one wave of a chunk
-// workgroup leaves for its row's merge workgroup, 64 bytes, tag stored last.
+// Streaming fast path (plh_stream.hip): the record one wave of a chunk
+// workgroup leaves for its row's merge workgroup.
 struct WaveRec {
   double m;        // greedy: the segment's largest penalised logit; temperature and top-p:
                    // its max y = z / T; top-k: its max z
@@ -66,22 +66,18 @@ struct WaveRec {
                    // candidates are all below theta)
   int n;           // greedy: the argmax's token id; top-k and top-p: candidates the wave wrote
   int flags;       // nonzero: the row needs the general pipeline
-  uint32_t tag;    // the generation of the call that wrote the record (stored last)
-  int pad[7];
 };
 constexpr int kCapW = 192;           // candidate slots of one wave's segment
 constexpr int kMaxStreamChunks = 64; // chunks per row at most (V <= 262144)
 
 struct StreamWs {
-  WaveRec* rec;      // [B * C * 8]: zeroed when allocated, so only tags of earlier calls are found there
+  WaveRec* rec;      // [B * C * 8] one record per wave of every chunk
   void* cval;        // [B * C * 8 * kCapW] candidate values (input type; 0 for penalised ones)
   int32_t* cidx;     // [B * C * 8 * kCapW] candidate token ids (bit 31: penalised)
   uint32_t* gbits;   // [B * gwords] penalty bitmaps of rows the general pipeline finishes
   int C;             // chunks per row
-  int L;             // a row's merge follows the chunks of the row L rows later in its stream
   int ncand;         // top-p rows: candidates one chunk aims at (the row's merge holds C * ncand)
   int gwords;        // words of one row's bitmap
-  uint32_t gen;      // this call's tag
 };
 
 struct SampleArgs {
@@ -100,8 +96,8 @@ struct SampleArgs {
   double* out_probs;
   unsigned long long* fallback_rows;  // rows finished by the general path
   int nucleus;                        // 1: eligible rows take the nucleus path
-  ChunkWs ws;                         // two-launch fast path only
-  StreamWs sw;                        // one-launch fast path only
+  ChunkWs ws;                         // chunk-partials fast path only
+  StreamWs sw;                        // streaming fast path only
 };
 
 struct DrawArgs {
@@ -165,13 +161,13 @@ ChunkWs fast_ws_layout(void* base, int B, int V, bool f64);
 // not null, is recorded on s between the two kernels.
 hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, int num_cu, hipStream_t s,
                               hipEvent_t between = nullptr);
-// One-launch fast path: bytes of the record region (zeroed when allocated)
-// and of the candidate region, their layout, and the launch (a.sw filled
-// by the caller: layout, gen).
-size_t stream_rec_bytes(int B, int V, bool f64);
+// Streaming fast path: workspace bytes (records, candidates, bitmaps), its
+// layout inside `ws` (256-byte aligned), and the two launches (chunks, then
+// one merge per row); `between`, when not null, is recorded on s between them.
 size_t stream_ws_bytes(int B, int V, bool f64);
-StreamWs stream_ws_layout(void* rec, void* ws, int B, int V, bool f64);
-hipError_t launch_sample_stream(const SampleArgs& a, bool f64, bool vec, hipStream_t s);
+StreamWs stream_ws_layout(void* ws, int B, int V, bool f64);
+hipError_t launch_sample_stream(const SampleArgs& a, bool f64, bool vec, hipStream_t s,
+                                hipEvent_t between = nullptr);
 hipError_t launch_draw(const DrawArgs& a, bool f64, hipStream_t s);
 hipError_t launch_penalize(const PenalizeArgs& a, bool f64, hipStream_t s);
 // Verify: workspace bytes for B rows of V tokens, its layout, and the two

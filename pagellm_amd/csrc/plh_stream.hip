@@ -1,38 +1,25 @@
-// One-launch sampler fast path for gfx950 (src/pagellm/engine/sampling.py:52-111).
-//
-// One grid holds two kinds of workgroups:
-//   chunk  workgroups read one 64 KB chunk of a row once (16-byte loads,
-//          32 fp32 or 16 fp64 tokens per thread), penalise it, and leave one
-//          record per wave (its 1/8 of the chunk, a "segment"), plus the
-//          segment's candidate tokens for rows that select:
+// Streaming sampler fast path for gfx950 (src/pagellm/engine/sampling.py:52-111),
+// two launches:
+//   k_stream_chunks  B x C workgroups: workgroup (row, c) reads the c-th
+//          64 KB chunk of the row once (16-byte loads, 32 fp32 or 16 fp64
+//          tokens per thread), penalises it, and leaves one record per wave
+//          (its 1/8 of the chunk, a "segment"), plus the segment's candidate
+//          tokens for rows that select:
 //            greedy       the segment's argmax;
 //            temperature  max y and sum exp(y - max) of the segment (y = z/T);
 //            top-k        tokens >= the chunk's threshold theta, taken from
 //                         the per-thread maxima so that it sits at or below
 //                         the chunk's k-th largest token;
-//            top-p        the segment's max and sums, and the tokens of a
-//                         window of value bins that brackets the chunk's
-//                         own top-p cut; the tokens above the window are
-//                         summed, not stored.
-//   merge  workgroups, one per row, wait for the row's records (each
-//          carries the generation tag of the call, stored after its data),
-//          then select exactly (k-th largest with ties, fixed-point top-p
-//          cut in (p descending, index ascending) order, fixed-point or
-//          float64 inverse-CDF draw in vocabulary order) and write the id.
-//          A row the records cannot decide exactly is finished by the
-//          general pipeline in the same workgroup.
-// Chunk and merge workgroups of a row are placed in the same one of eight
-// interleaved streams of block ids (block b belongs to stream b % 8, the
-// XCD the hardware dispatcher gives it), so a row's records and its
-// history are shared through one L2; a row's merge comes a few rows after
-// its chunks in its stream, so it rarely waits and every merge but the last
-// few overlaps other rows' streaming.  A merge waits only on blocks with
-// lower ids in its stream, with a bounded wait: past it, the merge computes
-// the row from the logits itself.
-//
-// Records and candidates are written with device-scope stores and read with
-// device-scope loads (coherent across XCDs without a cache writeback); a
-// wave stores its tag only after its own stores have completed.
+//            top-p        the segment's max and sum, and the tokens at or
+//                         above a threshold picked from a value histogram
+//                         so that the chunk keeps about ncand of them.
+//   k_stream_merge   one workgroup per row selects exactly from the
+//          records (k-th largest with ties, fixed-point top-p cut in
+//          (p descending, index ascending) order, fixed-point or float64
+//          inverse-CDF draw in vocabulary order) and writes the id.  A row
+//          the records cannot decide exactly (a threshold above the cut, a
+//          candidate overflow) is finished by the general pipeline in the
+//          same workgroup.
 #include <type_traits>
 
 #include "plh_fast.h"
@@ -55,8 +42,6 @@ constexpr int kFinal = 64;         // entries a selection ranks directly
 constexpr double kRangeY = 40.0;   // histogram span below the chunk max, in units of y = z/T
 constexpr int kMaxSegs = kMaxStreamChunks * kWaves;
 constexpr uint32_t kPenBit = 0x80000000u;  // candidate id flag: the token was penalised
-constexpr uint32_t kTagBits = 0x40000000u; // set in every tag (never a zeroed record's)
-constexpr long long kWaitTicks = 20000000;  // 200 ms of the 100 MHz real-time counter
 
 enum : int { kModeGreedy = 0, kModeTemp = 1, kModeTopK = 2, kModeTopP = 3, kModeGeneral = 4 };
 enum : int { kRecIncomplete = 1, kRecOverflow = 2 };
@@ -119,44 +104,12 @@ struct MergeLds {
   double ctld[4];
 };
 
-union StreamLds {
-  ChunkLds c;
+union MergeSmem {
   MergeLds m;
-  SmemCore g;
+  SmemCore g;  // the general pipeline (rows the records cannot decide)
 };
 
 // ------------------------------------------------------- device helpers
-
-__device__ __forceinline__ void st_dev(double* p, double v) {
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev(float* p, float v) {
-  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev(int* p, int v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ double ld_dev(const double* p) {
-  return __builtin_bit_cast(double, __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT));
-}
-__device__ __forceinline__ float ld_dev(const float* p) {
-  return __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT));
-}
-__device__ __forceinline__ int ld_dev(const int* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Every store the calling wave has issued is complete (and, being a
-// device-scope store, visible to every CU) before the next instruction.
-__device__ __forceinline__ void wave_stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 __device__ __forceinline__ RowParams stream_row_params(const SampleArgs& a, int row) {
   RowParams rp;
@@ -180,49 +133,6 @@ __device__ __forceinline__ int row_mode(const RowParams& rp) {
   if (rp.topk) return rp.top_k <= kTopkMax ? kModeTopK : kModeGeneral;
   if (rp.topp) return kModeTopP;
   return kModeTemp;
-}
-
-// Block b -> (kind, row, chunk).  Stream x = b % 8 holds rows x, x+8, ...
-// (local rows 0..R_x-1): the chunks of local row i, then the merge of local
-// row i - L; the last L merges close the stream.  kind 0: nothing to do.
-struct Item {
-  int kind;  // 0 idle, 1 chunk, 2 merge
-  int row, chunk;
-};
-
-__device__ __forceinline__ Item item_of(const StreamWs& w, int B, int b) {
-  const int x = b & 7, j = b >> 3;
-  const int Rx = (B - x + 7) >> 3;
-  const int C = w.C;
-  const int Lx = min(w.L, Rx);
-  Item it{0, 0, 0};
-  int li;
-  if (j < Lx * C) {
-    li = j / C;
-    it.kind = 1;
-    it.chunk = j - li * C;
-  } else {
-    const int jp = j - Lx * C;
-    const int mid = (Rx - Lx) * (C + 1);
-    if (jp < mid) {
-      const int q = jp / (C + 1), k = jp - q * (C + 1);
-      if (k < C) {
-        li = Lx + q;
-        it.kind = 1;
-        it.chunk = k;
-      } else {
-        li = q;
-        it.kind = 2;
-      }
-    } else {
-      const int t = jp - mid;
-      if (t >= Lx) return it;
-      li = Rx - Lx + t;
-      it.kind = 2;
-    }
-  }
-  it.row = x + 8 * li;
-  return it;
 }
 
 // ================================================================ chunks
@@ -388,8 +298,8 @@ __device__ __forceinline__ int write_cands(const Toks<TIn>& tk, const Flag& flag
   for (int e = 0; e < G::EPT; ++e) {
     const TIn v = tk.rv(e);
     if (flag(e, v)) {
-      st_dev(cv + slot, v);
-      st_dev(ci + slot, slot_tok<TIn>(c0, e));
+      cv[slot] = v;
+      ci[slot] = slot_tok<TIn>(c0, e);
       ++slot;
     }
   }
@@ -398,8 +308,8 @@ __device__ __forceinline__ int write_cands(const Toks<TIn>& tk, const Flag& flag
       // the raw input value and the penalised flag: the merge recomputes the
       // penalised value with the same arithmetic
       const int tok = cm.pt[wave()][tk.po + i];
-      st_dev(cv + slot, (TIn)0);
-      st_dev(ci + slot, (int)((uint32_t)tok | kPenBit));
+      cv[slot] = (TIn)0;
+      ci[slot] = (int)((uint32_t)tok | kPenBit);
       ++slot;
     }
   }
@@ -408,16 +318,7 @@ __device__ __forceinline__ int write_cands(const Toks<TIn>& tk, const Flag& flag
 
 __device__ __forceinline__ void publish(const SampleArgs& a, size_t gw, double m, double s, double th, int n,
                                         int flags) {
-  WaveRec* r = a.sw.rec + gw;
-  if (lane() == 0) {
-    st_dev(&r->m, m);
-    st_dev(&r->s, s);
-    st_dev(&r->a, th);
-    st_dev(&r->n, n);
-    st_dev(&r->flags, flags);
-  }
-  wave_stores_done();
-  if (lane() == 0) st_dev(&r->tag, a.sw.gen);
+  if (lane() == 0) a.sw.rec[gw] = WaveRec{m, s, th, n, flags};
 }
 
 // Each wave walks the kNB bins of cm.hist from bin 0 on its own: the first
@@ -442,6 +343,11 @@ __device__ __forceinline__ int hist_reach(const ChunkLds& cm, uint32_t k) {
 template <typename TIn, bool VEC>
 __device__ __forceinline__ void chunk_phase(const SampleArgs& a, int row, int c, ChunkLds& cm) {
   using G = SGeo<TIn>;
+  // the chunk's loads go out first: the row's parameters arrive meanwhile
+  const int c0 = c * G::CH;
+  const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
+  Toks<TIn> tk;
+  load_toks<TIn, VEC>(x, a.V, c0, tk);
   const RowParams rp = stream_row_params(a, row);
   const int mode = row_mode(rp);
   const size_t gw = ((size_t)row * a.sw.C + c) * kWaves + wave();
@@ -449,10 +355,6 @@ __device__ __forceinline__ void chunk_phase(const SampleArgs& a, int row, int c,
     publish(a, gw, -INFINITY, 0.0, 0.0, 0, 0);
     return;
   }
-  const int c0 = c * G::CH;
-  const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
-  Toks<TIn> tk;
-  load_toks<TIn, VEC>(x, a.V, c0, tk);
   int flags = 0;
   if (rp.pen_active) {
     const uint32_t pb = chunk_pen_bits<TIn>(a, rp, c0, cm);
@@ -504,7 +406,9 @@ __device__ __forceinline__ void chunk_phase(const SampleArgs& a, int row, int c,
     for (int e = 0; e < G::EPT; e += 2) {
       s0 += exp_neg_term(fma((double)tk.rv(e), invT, -my), tab);
       s1 += exp_neg_term(fma((double)tk.rv(e + 1), invT, -my), tab);
-      __builtin_amdgcn_sched_barrier(0);
+      // each pair of terms is complete here: the table loads of later
+      // tokens are not hoisted (they would be held as 64-bit registers)
+      asm volatile("" : "+v"(s0), "+v"(s1));
     }
     for (int i = 0; i < tk.np; ++i) s0 += exp_neg_term(fma(pz[i], invT, -my), tab);
     s = wave_sum(s0 + s1);
@@ -605,38 +509,13 @@ __device__ __forceinline__ RowRec load_rec(const SampleArgs& a, int row, int nse
   const int t = threadIdx.x;
   if (t < nseg) {
     const WaveRec* p = a.sw.rec + (size_t)row * nseg + t;
-    r.m = ld_dev(&p->m);
-    r.s = ld_dev(&p->s);
-    r.a = ld_dev(&p->a);
-    r.n = ld_dev(&p->n);
-    r.flags = ld_dev(&p->flags);
+    r.m = p->m;
+    r.s = p->s;
+    r.a = p->a;
+    r.n = p->n;
+    r.flags = p->flags;
   }
   return r;
-}
-
-// Waits until every record of the row carries this call's tag; false after
-// kWaitTicks (the caller then computes the row itself).
-__device__ __forceinline__ bool wait_row(const SampleArgs& a, int row, int nseg, MergeLds& ml) {
-  if (wave() == 0) {
-    const WaveRec* base = a.sw.rec + (size_t)row * nseg;
-    const long long t0 = (long long)__builtin_amdgcn_s_memrealtime();
-    bool ok = false;
-    for (;;) {
-      bool mine = true;
-      for (int i = lane(); i < nseg; i += kWave) mine &= ld_dev(&base[i].tag) == a.sw.gen;
-      if (__all(mine)) {
-        ok = true;
-        break;
-      }
-      if ((long long)__builtin_amdgcn_s_memrealtime() - t0 > kWaitTicks) break;
-      __builtin_amdgcn_s_sleep(2);
-    }
-    if (lane() == 0) ml.ctl[0] = ok ? 1 : 0;
-  }
-  wg_barrier();
-  const bool ok = ml.ctl[0] != 0;
-  wg_barrier();
-  return ok;
 }
 
 // A row's candidates in a merge: entry s of thread t is candidate
@@ -663,13 +542,13 @@ __device__ __forceinline__ size_t cand_slot(const MergeLds& ml, int row, int nse
 // Candidate j's token id and penalised logit z.
 template <typename TIn>
 __device__ __forceinline__ int cand_z(const SampleArgs& a, int row, double pen, size_t slot, double* z) {
-  const uint32_t id = (uint32_t)ld_dev(a.sw.cidx + slot);
+  const uint32_t id = (uint32_t)a.sw.cidx[slot];
   const int tok = (int)(id & ~kPenBit);
   if (id & kPenBit) {
     const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
     *z = penalize((double)x[tok], pen);
   } else {
-    *z = (double)ld_dev(reinterpret_cast<const TIn*>(a.sw.cval) + slot);
+    *z = (double)reinterpret_cast<const TIn*>(a.sw.cval)[slot];
   }
   return tok;
 }
@@ -795,7 +674,7 @@ __device__ __forceinline__ SelOut select_desc(Cands& cd, const SampleArgs& a, in
         ml.fkey[slot] = cd.key[s];
         ml.fw[slot] = wgt(s);
         const int j = (int)threadIdx.x + s * kThreads;
-        ml.fidx[slot] = (int)((uint32_t)ld_dev(a.sw.cidx + cand_slot(ml, row, nseg, j)) & ~kPenBit);
+        ml.fidx[slot] = (int)((uint32_t)a.sw.cidx[cand_slot(ml, row, nseg, j)] & ~kPenBit);
       }
     }
   wg_barrier();
@@ -945,7 +824,7 @@ __device__ __forceinline__ int draw_rescan_temp(const SampleArgs& a, const RowPa
 }
 
 template <typename TIn, bool VEC>
-__device__ __forceinline__ void merge_general(const SampleArgs& a, int row, const RowParams& rp, StreamLds& sm) {
+__device__ __forceinline__ void merge_general(const SampleArgs& a, int row, const RowParams& rp, MergeSmem& sm) {
   uint32_t* bits = a.sw.gbits + (size_t)row * a.sw.gwords;
   if (rp.pen_active) build_bitmap_global(bits, a.V, a.hist_ids, rp.h0, rp.h1);
   const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
@@ -960,19 +839,20 @@ __device__ __forceinline__ void merge_general(const SampleArgs& a, int row, cons
 }
 
 template <typename TIn, bool VEC>
-__device__ __forceinline__ void merge_phase(const SampleArgs& a, int row, StreamLds& sm) {
+__device__ __forceinline__ void merge_phase(const SampleArgs& a, int row, MergeSmem& sm) {
   using G = SGeo<TIn>;
   MergeLds& ml = sm.m;
-  const RowParams rp = stream_row_params(a, row);
-  const int mode = row_mode(rp);
   const int C = a.sw.C;
   const int nseg = C * kWaves;
-  if (mode == kModeGeneral || !wait_row(a, row, nseg, ml)) {
+  // the records and the row's parameters are loaded together
+  const RowRec r = load_rec(a, row, nseg);
+  const RowParams rp = stream_row_params(a, row);
+  const int mode = row_mode(rp);
+  if (mode == kModeGeneral) {
     merge_general<TIn, VEC>(a, row, rp, sm);
     return;
   }
   if (threadIdx.x < 64) ml.exp_tab[threadIdx.x] = kExp2Frac64[threadIdx.x];
-  const RowRec r = load_rec(a, row, nseg);
   // a segment flagged (or a count no wave can have written): the row needs
   // the general pipeline
   const bool cand_mode = mode == kModeTopK || mode == kModeTopP;
@@ -1167,7 +1047,7 @@ __device__ __forceinline__ void merge_phase(const SampleArgs& a, int row, Stream
         if (cut) {
           int id = INT_MAX;
           if (cd.key[s] == cut_key)  // ties at the cut are ranked by token id
-            id = (int)((uint32_t)ld_dev(a.sw.cidx + ((size_t)row * nseg + g) * kCapW + (j - ml.segoff[g])) & ~kPenBit);
+            id = (int)((uint32_t)a.sw.cidx[((size_t)row * nseg + g) * kCapW + (j - ml.segoff[g])] & ~kPenBit);
           keep = cd.key[s] > cut_key || (cd.key[s] == cut_key && id <= cut_idx);
         }
         if (keep) lds_add(&ml.segm[g], to_fx(__builtin_bit_cast(double, cd.key[s])));
@@ -1207,16 +1087,19 @@ __device__ __forceinline__ void merge_phase(const SampleArgs& a, int row, Stream
   if (t == 0) a.out_ids[row] = id;
 }
 
+// Grid B * C: block b is chunk b % C of row b / C.
 template <typename TIn, bool VEC>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_sample_stream(SampleArgs a) {
-  __shared__ StreamLds sm;
-  const Item it = item_of(a.sw, a.B, blockIdx.x);
-  if (it.kind == 0) return;
-  if (it.kind == 1) {
-    chunk_phase<TIn, VEC>(a, it.row, it.chunk, sm.c);
-    return;
-  }
-  merge_phase<TIn, VEC>(a, it.row, sm);
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_stream_chunks(SampleArgs a) {
+  __shared__ ChunkLds sm;
+  const int row = (int)blockIdx.x / a.sw.C;
+  chunk_phase<TIn, VEC>(a, row, (int)blockIdx.x - row * a.sw.C, sm);
+}
+
+// Grid B: block b merges row b.
+template <typename TIn, bool VEC>
+__global__ __launch_bounds__(kThreads) void k_stream_merge(SampleArgs a) {
+  __shared__ MergeSmem sm;
+  merge_phase<TIn, VEC>(a, (int)blockIdx.x, sm);
 }
 
 size_t up256s(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -1225,28 +1108,26 @@ size_t up256s(size_t v) { return (v + 255) & ~(size_t)255; }
 
 int stream_chunk_tokens(bool f64) { return f64 ? SGeo<double>::CH : SGeo<float>::CH; }
 
-size_t stream_rec_bytes(int B, int V, bool f64) {
-  const int CH = stream_chunk_tokens(f64);
-  const size_t C = (size_t)((V + CH - 1) / CH);
-  return up256s((size_t)B * C * kWaves * sizeof(WaveRec));
-}
-
 size_t stream_ws_bytes(int B, int V, bool f64) {
   const int CH = stream_chunk_tokens(f64);
   const size_t C = (size_t)((V + CH - 1) / CH);
-  const size_t nslot = (size_t)B * C * kWaves * kCapW;
+  const size_t nseg = (size_t)B * C * kWaves;
+  const size_t nslot = nseg * kCapW;
   const size_t gwords = (size_t)((V + 31) / 32);
-  return up256s(nslot * (f64 ? 8 : 4)) + up256s(nslot * 4) + up256s((size_t)B * gwords * 4);
+  return up256s(nseg * sizeof(WaveRec)) + up256s(nslot * (f64 ? 8 : 4)) + up256s(nslot * 4) +
+         up256s((size_t)B * gwords * 4);
 }
 
-StreamWs stream_ws_layout(void* rec, void* ws, int B, int V, bool f64) {
+StreamWs stream_ws_layout(void* ws, int B, int V, bool f64) {
   StreamWs w{};
   const int CH = stream_chunk_tokens(f64);
   w.C = (V + CH - 1) / CH;
-  const size_t nslot = (size_t)B * w.C * kWaves * kCapW;
+  const size_t nseg = (size_t)B * w.C * kWaves;
+  const size_t nslot = nseg * kCapW;
   w.gwords = (V + 31) / 32;
-  w.rec = static_cast<WaveRec*>(rec);
   char* p = static_cast<char*>(ws);
+  w.rec = reinterpret_cast<WaveRec*>(p);
+  p += up256s(nseg * sizeof(WaveRec));
   w.cval = p;
   p += up256s(nslot * (f64 ? 8 : 4));
   w.cidx = reinterpret_cast<int32_t*>(p);
@@ -1257,19 +1138,30 @@ StreamWs stream_ws_layout(void* rec, void* ws, int B, int V, bool f64) {
   // (the histogram counts every VW-th token: the chunk's actual count can
   // exceed the target by a few percent)
   w.ncand = min((int)(0.85 * kCandMax / w.C), (int)(0.6 * kWaves * kCapW));
-  w.L = 4;
   return w;
 }
 
-hipError_t launch_sample_stream(const SampleArgs& a, bool f64, bool vec, hipStream_t s) {
-  const int R = (a.B + 7) / 8;
-  const dim3 grid(8 * R * (a.sw.C + 1)), block(kThreads);
+hipError_t launch_sample_stream(const SampleArgs& a, bool f64, bool vec, hipStream_t s, hipEvent_t between) {
+  const dim3 gc(a.B * a.sw.C), gm(a.B), block(kThreads);
   if (f64) {
-    if (vec) hipLaunchKernelGGL((k_sample_stream<double, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((k_sample_stream<double, false>), grid, block, 0, s, a);
+    if (vec) hipLaunchKernelGGL((k_stream_chunks<double, true>), gc, block, 0, s, a);
+    else hipLaunchKernelGGL((k_stream_chunks<double, false>), gc, block, 0, s, a);
   } else {
-    if (vec) hipLaunchKernelGGL((k_sample_stream<float, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((k_sample_stream<float, false>), grid, block, 0, s, a);
+    if (vec) hipLaunchKernelGGL((k_stream_chunks<float, true>), gc, block, 0, s, a);
+    else hipLaunchKernelGGL((k_stream_chunks<float, false>), gc, block, 0, s, a);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (between != nullptr) {
+    e = hipEventRecord(between, s);
+    if (e != hipSuccess) return e;
+  }
+  if (f64) {
+    if (vec) hipLaunchKernelGGL((k_stream_merge<double, true>), gm, block, 0, s, a);
+    else hipLaunchKernelGGL((k_stream_merge<double, false>), gm, block, 0, s, a);
+  } else {
+    if (vec) hipLaunchKernelGGL((k_stream_merge<float, true>), gm, block, 0, s, a);
+    else hipLaunchKernelGGL((k_stream_merge<float, false>), gm, block, 0, s, a);
   }
   return hipGetLastError();
 }
