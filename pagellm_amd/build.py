@@ -19,7 +19,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OUT = PKG / "libpagellm_hip.so"
 BUILD = PKG / "_build"
-SOURCES = ["plh_sample.hip", "plh_stream.hip", "plh_verify.hip", "plh_head.hip", "plh_api.hip"]
+SOURCES = ["plh_sample.hip", "plh_verify.hip", "plh_head.hip", "plh_api.hip"]
 HEADERS = ["plh_device.h", "plh_pipeline.h", "plh_kernels.h"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

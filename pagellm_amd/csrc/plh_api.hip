@@ -4,8 +4,6 @@
 #include <string.h>
 
 #include <array>
-#include <atomic>
-#include <cstdlib>
 #include <mutex>
 #include <new>
 #include <string>
@@ -30,7 +28,6 @@ struct plh_ctx {
   hipStream_t ws_stream = nullptr;
   // plh_sample_noalloc: this device's copy of the file-scope scratch array
   void* scratch = nullptr;
-  bool stream_path = false;  // PLH_STREAM_PATH=1: the streaming kernels
   // PLH_OPT_KERNEL_TIMING: event triples (start, between, end) per timed call
   bool timing = false;
   std::vector<hipEvent_t> ev_free;
@@ -195,50 +192,26 @@ int sample_impl(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, in
     if (e != hipSuccess) return hip_fail(c, e, "plh_sample launch");
     return PLH_OK;
   }
-  // rows whose nucleus holds most of the vocabulary (the caller's
-  // PLH_SAMPLE_NUCLEUS hint) take the multi-pass nucleus kernels
-  if (!c->stream_path || (flags & PLH_SAMPLE_NUCLEUS)) {
-    const size_t need = plh::fast_ws_bytes(B, V, f64);
-    if (noalloc) {
-      if (need > kScratchBytes) return fail(c, PLH_ERR_INVALID_ARG, "batch too large for plh_sample_noalloc%s");
-      a.ws = plh::fast_ws_layout(c->scratch, B, V, f64);
-      const hipError_t e = plh::launch_sample_fast(a, f64, vec, c->num_cu, c->stream, nullptr);
-      if (e != hipSuccess) return hip_fail(c, e, "plh_sample_noalloc launch");
-      return PLH_OK;
-    }
-    rc = reserve_ws(c, need);
-    if (rc != PLH_OK) return rc;
-    a.ws = plh::fast_ws_layout(c->ws, B, V, f64);
-    std::array<hipEvent_t, 3> ev{};
-    rc = timing_begin(c, ev);
-    if (rc != PLH_OK) return rc;
-    const hipError_t e = plh::launch_sample_fast(a, f64, vec, c->num_cu, c->stream, ev[1]);
-    if (e != hipSuccess) return hip_fail(c, e, "plh_sample launch");
-    if (c->timing) PLH_HIP(c, hipEventRecord(ev[2], c->stream), "hipEventRecord");
-    PLH_HIP(c, hipEventRecord(c->ws_done, c->stream), "hipEventRecord");
-    c->ws_stream = c->stream;
-    return PLH_OK;
-  }
-  const size_t need = plh::stream_ws_bytes(B, V, f64);
+  const size_t need = plh::fast_ws_bytes(B, V, f64);
   if (noalloc) {
     if (need > kScratchBytes) {
-      char msg[200];
+      char msg[160];
       snprintf(msg, sizeof(msg), "this batch needs %zu bytes of workspace; plh_sample_noalloc holds %zu%%s", need,
                kScratchBytes);
       return fail(c, PLH_ERR_INVALID_ARG, msg);
     }
-    a.sw = plh::stream_ws_layout(c->scratch, B, V, f64);
-    const hipError_t e = plh::launch_sample_stream(a, f64, vec, c->stream, nullptr);
+    a.ws = plh::fast_ws_layout(c->scratch, B, V, f64);
+    const hipError_t e = plh::launch_sample_fast(a, f64, vec, c->num_cu, c->stream, nullptr);
     if (e != hipSuccess) return hip_fail(c, e, "plh_sample_noalloc launch");
     return PLH_OK;
   }
   rc = reserve_ws(c, need);
   if (rc != PLH_OK) return rc;
-  a.sw = plh::stream_ws_layout(c->ws, B, V, f64);
+  a.ws = plh::fast_ws_layout(c->ws, B, V, f64);
   std::array<hipEvent_t, 3> ev{};
   rc = timing_begin(c, ev);
   if (rc != PLH_OK) return rc;
-  const hipError_t e = plh::launch_sample_stream(a, f64, vec, c->stream, ev[1]);
+  const hipError_t e = plh::launch_sample_fast(a, f64, vec, c->num_cu, c->stream, ev[1]);
   if (e != hipSuccess) return hip_fail(c, e, "plh_sample launch");
   if (c->timing) PLH_HIP(c, hipEventRecord(ev[2], c->stream), "hipEventRecord");
   PLH_HIP(c, hipEventRecord(c->ws_done, c->stream), "hipEventRecord");
@@ -272,8 +245,6 @@ int plh_create(plh_ctx** out, int device) {
     if (hipDeviceGetAttribute(&c->num_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
         c->num_cu <= 0) { rc = PLH_ERR_HIP; break; }
     rc = resolve_scratch(c);
-    const char* sp = getenv("PLH_STREAM_PATH");
-    c->stream_path = sp != nullptr && sp[0] == '1';
   } while (0);
   if (rc != PLH_OK) {
     plh_destroy(c);

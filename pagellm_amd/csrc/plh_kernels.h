@@ -56,30 +56,6 @@ struct ChunkWs {
   int capc;         // candidate slots per chunk
 };
 
-// Streaming fast path (plh_stream.hip): the record one wave of a chunk
-// workgroup leaves for its row's merge workgroup.
-struct WaveRec {
-  double m;        // greedy: the segment's largest penalised logit; temperature and top-p:
-                   // its max y = z / T; top-k: its max z
-  double s;        // temperature and top-p: sum of exp(y - m) over the segment
-  double a;        // top-k and top-p: the chunk's threshold theta (its tokens not kept as
-                   // candidates are all below theta)
-  int n;           // greedy: the argmax's token id; top-k and top-p: candidates the wave wrote
-  int flags;       // nonzero: the row needs the general pipeline
-};
-constexpr int kCapW = 192;           // candidate slots of one wave's segment
-constexpr int kMaxStreamChunks = 64; // chunks per row at most (V <= 262144)
-
-struct StreamWs {
-  WaveRec* rec;      // [B * C * 8] one record per wave of every chunk
-  void* cval;        // [B * C * 8 * kCapW] candidate values (input type; 0 for penalised ones)
-  int32_t* cidx;     // [B * C * 8 * kCapW] candidate token ids (bit 31: penalised)
-  uint32_t* gbits;   // [B * gwords] penalty bitmaps of rows the general pipeline finishes
-  int C;             // chunks per row
-  int ncand;         // top-p rows: candidates one chunk aims at (the row's merge holds C * ncand)
-  int gwords;        // words of one row's bitmap
-};
-
 struct SampleArgs {
   const void* logits;
   int64_t ld;
@@ -96,8 +72,7 @@ struct SampleArgs {
   double* out_probs;
   unsigned long long* fallback_rows;  // rows finished by the general path
   int nucleus;                        // 1: eligible rows take the nucleus path
-  ChunkWs ws;                         // chunk-partials fast path only
-  StreamWs sw;                        // streaming fast path only
+  ChunkWs ws;                         // fast path only
 };
 
 struct DrawArgs {
@@ -161,13 +136,6 @@ ChunkWs fast_ws_layout(void* base, int B, int V, bool f64);
 // not null, is recorded on s between the two kernels.
 hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, int num_cu, hipStream_t s,
                               hipEvent_t between = nullptr);
-// Streaming fast path: workspace bytes (records, candidates, bitmaps), its
-// layout inside `ws` (256-byte aligned), and the two launches (chunks, then
-// one merge per row); `between`, when not null, is recorded on s between them.
-size_t stream_ws_bytes(int B, int V, bool f64);
-StreamWs stream_ws_layout(void* ws, int B, int V, bool f64);
-hipError_t launch_sample_stream(const SampleArgs& a, bool f64, bool vec, hipStream_t s,
-                                hipEvent_t between = nullptr);
 hipError_t launch_draw(const DrawArgs& a, bool f64, hipStream_t s);
 hipError_t launch_penalize(const PenalizeArgs& a, bool f64, hipStream_t s);
 // Verify: workspace bytes for B rows of V tokens, its layout, and the two

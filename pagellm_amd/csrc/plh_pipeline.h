@@ -26,10 +26,7 @@ constexpr int kBins = 2048;  // widest radix digit is 11 bits
 constexpr int kSmall = 512;  // a bin this small is finished by an LDS sort
 constexpr int kMaxVBitmap = 262144;  // penalty bitmap capacity (vocabulary size)
 
-// LDS of the pipeline (34.5 KB); Smem adds the row's penalty bitmap for
-// callers that keep it on chip (k_sample_rows), others keep it in global
-// memory and pass its address to the row source.
-struct SmemCore {
+struct Smem {
   double redd[kWaves];
   uint64_t redu[kWaves];
   uint32_t redw[kWaves];
@@ -43,9 +40,6 @@ struct SmemCore {
   uint64_t lw[kSmall];
   int32_t lidx[kSmall];
   double exp_tab[64];
-};
-
-struct Smem : SmemCore {
   uint32_t bitmap[kMaxVBitmap / 32];
 };
 
@@ -74,23 +68,6 @@ __device__ __forceinline__ void build_bitmap(uint32_t* bitmap, int lo, int n, co
   __syncthreads();
 }
 
-// build_bitmap for a bitmap in global memory (one row's, in a workspace
-// the calling workgroup owns): the same bits, set with device atomics.
-__device__ __forceinline__ void build_bitmap_global(uint32_t* bitmap, int n, const int32_t* ids, int64_t h0,
-                                                    int64_t h1) {
-  const int words = (n + 31) >> 5;
-  for (int w = threadIdx.x; w < words; w += kThreads)
-    __hip_atomic_store(bitmap + w, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __builtin_amdgcn_s_waitcnt(0);  // every wave's zeroing stores have completed ...
-  __syncthreads();                // ... before any wave's atomics
-  for (int64_t h = h0 + threadIdx.x; h < h1; h += kThreads) {
-    const int off = ids[h];
-    if ((unsigned)off < (unsigned)n) atomicOr(&bitmap[off >> 5], 1u << (off & 31));
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-}
-
 // p(z) of the processed distribution for tokens that survived top-k
 // (z >= z_lo); sampling.py:75-81, with y = z * (1 / T) and the table exp.
 struct PCalc {
@@ -110,13 +87,13 @@ __device__ __forceinline__ double p_of(const PCalc& c, double z) {
 // tokens base + 32t .. base + 32t + 31, loaded before any is used; f(j, z,
 // idx) is called for each of them in order (invalid ones: z = -inf, idx =
 // INT_MAX).
-template <typename TIn, bool VEC, bool GBITS = false, int PER = 32>
+template <typename TIn, bool VEC>
 struct RowSource {
-  static constexpr int kPer = PER;  // tokens per thread per group (a multiple of 8)
+  static constexpr int kPer = 32;
   static constexpr int kGroup = kPer * kThreads;
   const TIn* x;  // row base
   int V;
-  const uint32_t* bits;  // penalty bitmap over [0, V): LDS, or global memory (GBITS)
+  const uint32_t* bits;  // LDS penalty bitmap over [0, V)
   bool pen_on;           // false: no penalty, `bits` is not read
   double pen;
 
@@ -144,13 +121,8 @@ struct RowSource {
 #pragma unroll
       for (int j = 0; j < kPer; ++j) raw[j] = p0 + j < V ? x[p0 + j] : (TIn)(-INFINITY);
     }
-    uint32_t pb = 0u;  // p0 is a multiple of kPer (<= 32, dividing 32): its bits lie in one word
-    if (pen_on && p0 < V) {
-      // a bitmap in global memory was set with device atomics: read it at
-      // device scope, never from a stale L1 line
-      pb = GBITS ? __hip_atomic_load(bits + (p0 >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : bits[p0 >> 5];
-      pb >>= (p0 & 31);
-    }
+    uint32_t pb = 0u;  // p0 is a multiple of 32: its bits are one word
+    if (pen_on && p0 < V) pb = bits[p0 >> 5];
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const bool valid = p0 + j < V;
@@ -173,7 +145,7 @@ struct BinPick {
 };
 
 template <bool MASS>
-__device__ __forceinline__ BinPick pick_bin_desc(SmemCore& sm, int nb, uint64_t above, uint64_t target) {
+__device__ __forceinline__ BinPick pick_bin_desc(Smem& sm, int nb, uint64_t above, uint64_t target) {
   const int per = nb / kThreads;  // 4 or 2 bins per thread, highest bins first
   uint64_t v[4];
   uint64_t s = 0;
@@ -228,7 +200,7 @@ struct SelResult {
 // desc, idx asc) order; the result of a selection whose earlier levels put
 // `above` (count or mass) before the list.
 template <int MODE>
-__device__ __forceinline__ SelResult sorted_pick(uint64_t target, uint64_t above, SmemCore& sm) {
+__device__ __forceinline__ SelResult sorted_pick(uint64_t target, uint64_t above, Smem& sm) {
   const int n = min(sm.ctl_i[2], kSmall);
   int N = 2;
   while (N < n) N <<= 1;
@@ -297,7 +269,7 @@ __device__ __forceinline__ SelResult sorted_pick(uint64_t target, uint64_t above
 // found == false when the eligible total is below target (above then holds
 // that total).
 template <int MODE, class Visit>
-__device__ __forceinline__ SelResult radix_select(const Visit& visit, uint64_t target, SmemCore& sm) {
+__device__ __forceinline__ SelResult radix_select(const Visit& visit, uint64_t target, Smem& sm) {
   uint64_t prefix = 0, above = 0;
   uint32_t bincnt = 0;
   int done = 0;
@@ -364,7 +336,7 @@ __device__ __forceinline__ SelResult radix_select(const Visit& visit, uint64_t t
 // total); ties: more than kSmall elements share one value.
 template <int MODE, class Visit>
 __device__ __forceinline__ SelResult value_select(const Visit& visit, double zlo, double zhi, uint64_t target,
-                                                  SmemCore& sm) {
+                                                  Smem& sm) {
   const Affine af = make_affine(zlo, zhi, kBins);
   for (int b = threadIdx.x; b < kBins; b += kThreads) {
     sm.cnt[b] = 0u;
@@ -522,7 +494,7 @@ struct PipeIn {
 };
 
 template <class Src>
-__device__ __forceinline__ int row_pipeline(Src& src, const RowParams& rp, int V, PipeIn in, SmemCore& sm,
+__device__ __forceinline__ int row_pipeline(Src& src, const RowParams& rp, int V, PipeIn in, Smem& sm,
                                             double* probs_out) {
   const int n = src.n();
   constexpr int kG = Src::kGroup;

@@ -40,6 +40,11 @@ namespace plh {
 
 constexpr int kU = 8;             // 16-byte loads per thread per chunk
 constexpr int kHB = 1024;         // histogram bins
+// k_sample_chunks keeps its histogram's bin b at hpad(b): one pad word
+// after every 16 bins, so 64 lanes reading 16 consecutive bins each
+// (stride 17 words) hit distinct LDS banks.
+constexpr int kHBPad = kHB + kHB / 16;
+__device__ __forceinline__ int hpad(int b) { return b + (b >> 4); }
 constexpr int kCandCap = 8192;    // candidates one row gathers
 constexpr int kCapChunk = 1024;   // candidate slots per chunk, at most
 constexpr int kMaxChunks = 64;    // chunks per row, at most (V <= 262144)
@@ -176,7 +181,7 @@ struct ChunkSmem {
   int ctl[8];
   uint64_t ctlu[4];
   double exp_tab[kWaves][64];  // one copy per wave
-  uint32_t hcnt[kHB + 1];  // bin kHB: -inf tokens (never scanned)
+  uint32_t hcnt[kHBPad];  // value histogram, bin b at hpad(b)
   uint32_t bitmap[Geo<float>::kChunk / 32];
   double pz[kWaves][kPenPerWave];
   int pt[kWaves][kPenPerWave];
@@ -369,6 +374,30 @@ __device__ __forceinline__ TIn in_threshold(double theta) {
   else return fmax(theta, -1.7976931348623157e308);
 }
 
+// Every wave walks the kHB bins of a count histogram from the highest down
+// on its own (no barrier): the bin where the running count first reaches
+// target, -1 when the total stays below it.  Exactly one bin takes the
+// running count from below target to target or more.
+__device__ __forceinline__ int hist_reach_desc(const uint32_t* h, uint32_t target) {
+  constexpr int PL = kHB / kWave;  // lane l walks bins kHB-1-l*PL ... downwards
+  uint32_t c[PL], sum = 0;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    c[i] = h[hpad(kHB - 1 - (lane() * PL + i))];
+    sum += c[i];
+  }
+  const uint32_t inc = wave_scan_incl(sum, 0u, OpAdd{});
+  uint32_t run = inc - sum;
+  int d = -1;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    if (d < 0 && run < target && run + c[i] >= target) d = kHB - 1 - (lane() * PL + i);
+    run += c[i];
+  }
+  const uint64_t hb = __ballot(d >= 0);
+  return hb == 0ull ? -1 : lane_value(d, __builtin_ctzll(hb));
+}
+
 // Candidates of one chunk: every finite z >= theta, with theta below the
 // chunk's target-th largest token (all finite tokens when there are fewer).
 //   top-k, k <= 512: the k-th largest of the workgroup's 512 per-thread
@@ -381,8 +410,9 @@ __device__ __forceinline__ TIn in_threshold(double theta) {
 //     L (typically three quarters) take no LDS atomic; else L is the
 //     smallest finite token.
 // theta is the lower edge of the histogram bin holding the target-th
-// largest (cm.hcnt is zeroed at kernel start), so every token left out is
-// below theta, which serves as the chunk's bound on them.  The passes over
+// largest (cm.hcnt is zeroed at kernel start; every wave finds that bin on
+// its own), so every token left out is below theta, which serves as the
+// chunk's bound on them.  The passes over
 // the register tokens compare in the input precision (exact: a float
 // converts to float64 exactly).  Each wave writes its candidates to a range
 // of the chunk's slots and its part: the chunk's largest z, theta, the end
@@ -460,7 +490,7 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
     const InAffine<TIn> rf(af);
     double tlo = af.lo, tscale = af.scale;
     if (by_max) {
-      if (lmax > -INFINITY) lds_add(&cm.hcnt[af.bin(lmax)], 1u);
+      if (lmax > -INFINITY) lds_add(&cm.hcnt[hpad(af.bin(lmax))], 1u);
     } else {
       tlo = rf.lo();
       tscale = rf.scale();
@@ -470,18 +500,18 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
 #pragma unroll
       for (int e = 0; e < kEpt; ++e) {
         const TIn x = tk.rv(e);
-        if (x >= lin) lds_add(&cm.hcnt[rf.bin(x)], 1u);
+        if (x >= lin) lds_add(&cm.hcnt[hpad(rf.bin(x))], 1u);
       }
       for (int i = 0; i < tk.np; ++i) {
         const double z = tk.pen_z(cm, i);
-        if (z > -INFINITY && z >= lo) lds_add(&cm.hcnt[pf.bin(z)], 1u);
+        if (z > -INFINITY && z >= lo) lds_add(&cm.hcnt[hpad(pf.bin(z))], 1u);
       }
     }
     wg_barrier();
-    const Pick pk = pick_desc<false>(cm.hcnt, nullptr, kHB, 0, target, cm.redu, cm.ctl, cm.ctlu);
+    const int d = hist_reach_desc(cm.hcnt, (uint32_t)target);
     // every z with bin(z) >= d is >= lo + (d - 0.01) / scale (bin(z) is
     // floor((z - lo) * scale) up to rounding); bin 0 starts at lo
-    if (pk.found) theta = pk.d > 0 ? tlo + ((double)uniform(pk.d) - 0.01) / tscale : lo;
+    if (d >= 0) theta = d > 0 ? tlo + ((double)d - 0.01) / tscale : lo;
   }
   theta = uniform(theta);
   const TIn tin = in_threshold<TIn>(theta);
@@ -572,7 +602,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   load_chunk<TIn, VEC>(x, a.V, c0, tk.v);
   const bool cands = rp.topk || (rp.topp && !(NUC && rp.nucleus));
   if (cands) {  // ordered before use by the first barrier of chunk_candidates
-    for (int b = threadIdx.x; b < kHB + 1; b += kThreads) cm.hcnt[b] = 0u;
+    for (int b = threadIdx.x; b < kHBPad; b += kThreads) cm.hcnt[b] = 0u;
     if (threadIdx.x == 0) cm.cand_n = 0;
   }
   int flags = 0;
