@@ -1212,8 +1212,11 @@ struct FastOut {
 // chunk candidates.
 // Every candidate slot of the row into registers (slot i = q * kThreads + t;
 // consecutive lanes read consecutive addresses).
-__device__ __forceinline__ void gather_cands(const SampleArgs& a, int row, RegCands& rc) {
+// With wc (a wave's copy of the chunks' candidate counts), only the slots
+// that hold a candidate are read.
+__device__ __forceinline__ void gather_cands(const SampleArgs& a, int row, RegCands& rc, const int* wc = nullptr) {
   const int slots = a.ws.C * a.ws.capc;
+  const int csh = __ffs(a.ws.capc) - 1;  // capc is a power of two
   const size_t base = (size_t)row * slots;
 #pragma unroll
   for (int q = 0; q < kPerT; ++q) {
@@ -1221,7 +1224,7 @@ __device__ __forceinline__ void gather_cands(const SampleArgs& a, int row, RegCa
     rc.v[q] = 0.0;
     rc.idx[q] = 0;
     rc.w[q] = 0ull;
-    if (i < slots) {
+    if (i < slots && (wc == nullptr || (i & (a.ws.capc - 1)) < wc[i >> csh])) {
       rc.v[q] = a.ws.cz[base + i];
       rc.idx[q] = a.ws.ci[base + i];
     }
@@ -1339,14 +1342,18 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   }
   XWave xw{fs.xw, 0};
   int hgen = 0;
-  // global loads first: candidates, segment partials, then the wave parts
+  // global loads first: candidates (top-p rows, whose chunks fill nearly
+  // every slot), segment partials, then the wave parts; top-k rows then
+  // read only the slots their chunks filled (typically a few percent)
   RegCands rc;
-  if (cands) gather_cands(a, row, rc);
+  const bool gather_early = cands && !rp.topk;
+  if (gather_early) gather_cands(a, row, rc);
   SegLoad sg;
   if (!rp.greedy && !rp.topk) {
     load_segs(a, row, (a.V + Geo<TIn>::kSeg - 1) / Geo<TIn>::kSeg, sg);
   }
   const PartSum ps = scan_parts(a, row, rp.greedy, cands, fs);
+  if (cands && !gather_early) gather_cands(a, row, rc, fs.wcnt[wave()]);
   // a chunk that could not keep all its penalised tokens aside sends the
   // row to the general pipeline
   bool general = ps.flags != 0;
