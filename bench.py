@@ -219,9 +219,22 @@ def run_cpu_baseline(workload: str, rows: int, reps: int, ids_path: str | None =
 COPY_BYTES = 256 << 20
 
 
-def pmc_probe(workload: str) -> None:
+def _probe_rows(workload: str, group: int | None, B: int) -> list:
+    """Rows of a counter probe: the whole batch, or (mixed128k) one of its
+    four parameter groups of 64 rows, repeated to the batch size so the
+    chunk kernel runs a full grid of one row mode."""
+    if group is None:
+        return list(range(B))
+    if workload != "mixed128k" or not 0 <= group < 4:
+        raise SystemExit("--probe-group applies to mixed128k's four row groups (0-3)")
+    g = list(range(64 * group, 64 * group + 64))
+    return (g * (B // 64 + 1))[:B]
+
+
+def pmc_probe(workload: str, group: int | None = None) -> None:
     """A short run for counter collection: a copy of COPY_BYTES (the
-    calibration), then a few sampler steps."""
+    calibration), then a few sampler steps (all rows, or one row group)."""
+    import numpy as np
     import torch
 
     from pagellm_amd import _native, workloads
@@ -229,15 +242,18 @@ def pmc_probe(workload: str) -> None:
 
     w = workloads.WORKLOADS[workload]()
     B, V = w["logits"].shape
+    rows = _probe_rows(workload, group, B)
+    params = [w["params"][i] for i in rows]
+    contexts = [w["contexts"][i] for i in rows]
     dev = torch.device("cuda:0")
     ctx = _native.Context(0)
     ctx.set_stream(torch.cuda.current_stream().cuda_stream)
-    t, k, p, r = _pack_params(w["params"])
+    t, k, p, r = _pack_params(params)
     hint = _nucleus_hint(t, k, p, w["logits"].shape[1])
-    hist_ids, hist_off = _pack_histories(w["contexts"], w["params"], B, V)
-    x = torch.from_numpy(w["logits"]).to(dev)
+    hist_ids, hist_off = _pack_histories(contexts, params, B, V)
+    x = torch.from_numpy(np.ascontiguousarray(w["logits"][rows])).to(dev)
     d = {n: torch.from_numpy(a).to(dev) for n, a in
-         dict(t=t, k=k, p=p, r=r, u=w["uniforms"], ids=hist_ids, off=hist_off).items() if a is not None}
+         dict(t=t, k=k, p=p, r=r, u=w["uniforms"][rows], ids=hist_ids, off=hist_off).items() if a is not None}
     out = torch.empty(B, dtype=torch.int32, device=dev)
     src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
@@ -286,6 +302,49 @@ def traffic_from(workload: str, fetch_dir: str, write_dir: str, dst: Path | None
            "bytes_per_launch": res["FETCH_SIZE"]["bytes_per_launch"] + res["WRITE_SIZE"]["bytes_per_launch"],
            "algorithmic_bytes": workloads.algorithmic_bytes(w), "counters": res}
     dst = dst if dst is not None else ROOT / "profiles" / f"traffic_{workload}.json"
+    dst.write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out))
+    return out
+
+
+VALU_COUNTERS = ("SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_WAVES")
+
+
+def valu_from(workload: str, dirs: list, dst: Path | None = None) -> dict:
+    """Instructions per token of k_sample_chunks for each mixed128k row
+    group, from one rocprofv3 counter run per group (`--pmc SQ_INSTS_VALU
+    SQ_INSTS_SALU SQ_INSTS_LDS SQ_WAVES -- python3 bench.py --pmc-probe
+    --probe-group G`, G = 0..3 in the order given): wave instructions x 64
+    lanes / tokens per launch, written to profiles/valu_<workload>.json."""
+    import csv
+
+    from pagellm_amd import workloads
+    w = workloads.WORKLOADS[workload]()
+    B, V = w["logits"].shape
+    names = ["greedy", "top_k 50", "top_p 0.9", "top_k 40 + top_p 0.95 + T 0.6 + penalty 1.1"]
+    groups = []
+    for gi, folder in enumerate(dirs):
+        per = {}
+        for f in Path(folder).rglob("*counter_collection.csv"):
+            for r in csv.DictReader(open(f)):
+                if "k_sample_chunks" not in r["Kernel_Name"] or r["Counter_Name"] not in VALU_COUNTERS:
+                    continue
+                per.setdefault(r["Dispatch_Id"], {}).setdefault(r["Counter_Name"], 0.0)
+                per[r["Dispatch_Id"]][r["Counter_Name"]] += float(r["Counter_Value"])
+        if not per:
+            raise SystemExit(f"no k_sample_chunks counters in {folder}")
+        launches = list(per.values())
+        mean = {c: sum(x.get(c, 0.0) for x in launches) / len(launches) for c in VALU_COUNTERS}
+        tokens = B * V
+        groups.append({"group": gi, "rows": names[gi] if gi < len(names) else str(gi), "launches": len(launches),
+                       "per_launch": mean,
+                       "valu_per_token": mean["SQ_INSTS_VALU"] * 64 / tokens,
+                       "salu_per_token": mean["SQ_INSTS_SALU"] * 64 / tokens,
+                       "lds_per_token": mean["SQ_INSTS_LDS"] * 64 / tokens})
+    out = {"workload": workload, "kernel": "k_sample_chunks", "tokens_per_launch": B * V,
+           "note": "wave instructions x 64 lanes / tokens; each group's 64 rows repeated to 256",
+           "groups": groups}
+    dst = dst if dst is not None else ROOT / "profiles" / f"valu_{workload}.json"
     dst.write_text(json.dumps(out, indent=1) + "\n")
     print(json.dumps(out))
     return out
@@ -543,6 +602,9 @@ def main() -> None:
     ap.add_argument("--cpu-baseline-child", action="store_true")
     ap.add_argument("--gpu-ids", help="(child) .npz of the GPU ids each configuration produced")
     ap.add_argument("--pmc-probe", action="store_true", help="short run for rocprofv3 counter passes")
+    ap.add_argument("--probe-group", type=int, help="(--pmc-probe) one mixed128k row group, 0-3, repeated")
+    ap.add_argument("--valu-from", nargs="+", metavar="DIR",
+                    help="counter run folders of --pmc-probe --probe-group 0..3 -> profiles/valu_<workload>.json")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the other workloads (zipf32k, zipf152k, char65, spec32k verify)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
@@ -556,8 +618,11 @@ def main() -> None:
     if args.traffic_from:
         traffic_from(args.workload, *args.traffic_from)
         return
+    if args.valu_from:
+        valu_from(args.workload, args.valu_from)
+        return
     if args.pmc_probe:
-        pmc_probe(args.workload)
+        pmc_probe(args.workload, args.probe_group)
         return
     if args.only:
         kw = dict(steps=min(args.steps, 50), warmup=min(args.warmup, 5))
