@@ -310,7 +310,7 @@ def traffic_from(workload: str, fetch_dir: str, write_dir: str, dst: Path | None
 VALU_COUNTERS = ("SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_WAVES")
 
 
-def valu_from(workload: str, dirs: list, dst: Path | None = None) -> dict:
+def valu_from(workload: str, dirs: list, dst: Path | None = None, shape: tuple | None = None) -> dict:
     """Instructions per token of k_sample_chunks for each mixed128k row
     group, from one rocprofv3 counter run per group (`--pmc SQ_INSTS_VALU
     SQ_INSTS_SALU SQ_INSTS_LDS SQ_WAVES -- python3 bench.py --pmc-probe
@@ -318,9 +318,10 @@ def valu_from(workload: str, dirs: list, dst: Path | None = None) -> dict:
     lanes / tokens per launch, written to profiles/valu_<workload>.json."""
     import csv
 
-    from pagellm_amd import workloads
-    w = workloads.WORKLOADS[workload]()
-    B, V = w["logits"].shape
+    if shape is None:
+        from pagellm_amd import workloads
+        shape = workloads.WORKLOADS[workload]()["logits"].shape
+    B, V = shape
     names = ["greedy", "top_k 50", "top_p 0.9", "top_k 40 + top_p 0.95 + T 0.6 + penalty 1.1"]
     groups = []
     for gi, folder in enumerate(dirs):

@@ -55,6 +55,38 @@ def test_traffic_scaling_from_counter_runs(tmp_path):
     assert (tmp_path / "t.json").exists()
 
 
+def test_instructions_per_token_from_counter_runs(tmp_path):
+    """--valu-from: per row group, the k_sample_chunks counters averaged
+    over its launches, times 64 lanes, over the tokens of one launch."""
+    import bench
+
+    B, V = 4, 1000
+    dirs = []
+    for g in range(2):
+        folder = tmp_path / f"g{g}"
+        folder.mkdir()
+        with open(folder / "run_counter_collection.csv", "w", newline="") as f:
+            w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
+            w.writeheader()
+            for did, scale in ((10, 1.0), (11, 3.0)):  # two launches: their mean is taken
+                for c, v in (("SQ_INSTS_VALU", 500.0), ("SQ_INSTS_SALU", 100.0), ("SQ_INSTS_LDS", 10.0),
+                             ("SQ_WAVES", 8.0)):
+                    w.writerow({"Dispatch_Id": did, "Kernel_Name": "void plh::k_sample_chunks<float, true, false>()",
+                                "Counter_Name": c, "Counter_Value": v * scale * (g + 1)})
+            # another kernel's counters are ignored
+            w.writerow({"Dispatch_Id": 12, "Kernel_Name": "void plh::k_sample_final<float, true, false>()",
+                        "Counter_Name": "SQ_INSTS_VALU", "Counter_Value": 1e9})
+        dirs.append(str(folder))
+    out = bench.valu_from("mixed128k", dirs, dst=tmp_path / "v.json", shape=(B, V))
+    g0, g1 = out["groups"]
+    assert g0["launches"] == 2 and g0["rows"] == "greedy"
+    assert g0["valu_per_token"] == pytest.approx(1000.0 * 64 / (B * V))
+    assert g1["valu_per_token"] == pytest.approx(2000.0 * 64 / (B * V))
+    assert g1["salu_per_token"] == pytest.approx(400.0 * 64 / (B * V))
+    assert g0["lds_per_token"] == pytest.approx(20.0 * 64 / (B * V))
+    assert (tmp_path / "v.json").exists()
+
+
 def test_algorithmic_bytes_of_the_headline_workload():
     """4V per row of fp32 logits, 4H per history id of a penalised row, 48
     per row of parameters, uniform, offset and id."""
