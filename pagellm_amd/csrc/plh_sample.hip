@@ -282,7 +282,10 @@ template <typename TIn>
 struct ChunkToks {
   using G = Geo<TIn>;
   typename VecOf<TIn>::T v[kU];
-  int po = 0, np = 0;
+  // the lane's share of its wave's pool: entries lane(), lane() + 64, ...
+  // below the wave's count (whichever lane set a token aside), so a pass
+  // over the pool takes at most kPenPerWave / 64 steps per lane
+  int np = 0;
   __device__ __forceinline__ TIn rv(int e) const { return v[e / G::kVW][e % G::kVW]; }
   __device__ __forceinline__ double raw(int e) const { return (double)rv(e); }
   // Called at the start of each pass: the compiler must then widen the
@@ -292,26 +295,27 @@ struct ChunkToks {
 #pragma unroll
     for (int j = 0; j < kU; ++j) asm volatile("" : "+v"(v[j]));
   }
-  __device__ __forceinline__ double pen_z(const ChunkSmem& cm, int i) const { return cm.pz[wave()][po + i]; }
-  __device__ __forceinline__ int pen_tok(const ChunkSmem& cm, int i) const { return cm.pt[wave()][po + i]; }
+  __device__ __forceinline__ double pen_z(const ChunkSmem& cm, int i) const { return cm.pz[wave()][lane() + kWave * i]; }
+  __device__ __forceinline__ int pen_tok(const ChunkSmem& cm, int i) const { return cm.pt[wave()][lane() + kWave * i]; }
 };
 
 // Moves the calling wave's penalised tokens (bits pb of each lane) out of
 // the registers: their penalised float64 value goes to the wave's LDS pool,
-// the register slot to -inf.  Returns true when the pool overflows (the
-// chunk is then incomplete).
+// the register slot to -inf.  Every lane then takes its share of the pool
+// (ChunkToks::np).  Each token of the chunk is then in exactly one lane's
+// set (its registers or its share of the pool), so per-lane maxima stay
+// maxima of disjoint sets.  Returns true when the pool overflows (the chunk
+// is then incomplete).
 template <typename TIn>
 __device__ __forceinline__ bool set_aside_penalised(ChunkToks<TIn>& tk, uint32_t pb, double pen, int c0, ChunkSmem& cm) {
   using G = Geo<TIn>;
   const int n = __popc(pb);
   const int incl = wave_scan_incl(n, 0, OpAdd{});
   const int total = lane_value(incl, kWave - 1);
-  tk.po = incl - n;
   tk.np = 0;
   if (total > kPenPerWave) return true;
-  tk.np = n;
   if (pb != 0u) {
-    int k = tk.po;
+    int k = incl - n;
 #pragma unroll
     for (int e = 0; e < G::kEpt; ++e) {
       if ((pb >> e) & 1u) {
@@ -322,8 +326,13 @@ __device__ __forceinline__ bool set_aside_penalised(ChunkToks<TIn>& tk, uint32_t
       }
     }
   }
-  // penalised afterwards, a few entries per lane (a division each)
-  for (int i = 0; i < tk.np; ++i) cm.pz[wave()][tk.po + i] = penalize(cm.pz[wave()][tk.po + i], pen);
+  // the lane's share (a wave's own LDS writes complete in order), penalised
+  // with one division each
+  tk.np = total > lane() ? (total - lane() + kWave - 1) / kWave : 0;
+  for (int i = 0; i < tk.np; ++i) {
+    double& z = cm.pz[wave()][lane() + kWave * i];
+    z = penalize(z, pen);
+  }
   return false;
 }
 
