@@ -62,10 +62,9 @@ __device__ __forceinline__ double fast_exp_neg(double d, const double* tab) {
 // exp(d) for d <= 0 as a term of a normaliser sum: the reduction and
 // polynomial of fast_exp_neg, with k = rint(d * 64 / ln2) from the
 // magic-number rounding (adding 1.5 * 2^52 leaves k in the low mantissa
-// bits) and 2^(k >> 6) added to the exponent field instead of an ldexp.  d
-// is clamped at -708, where the scaled result is still normal: a term
-// below e^-708 (including -inf) counts as e^-708 ~ 3e-308, which no sum
-// holding a term of 1 can notice.
+// bits).  d is clamped at -708, where the scaled result is still normal: a
+// term below e^-708 (including -inf) counts as e^-708 ~ 3e-308, which no
+// sum holding a term of 1 can notice.
 constexpr double kExpMagic = 6755399441055744.0;  // 1.5 * 2^52
 
 __device__ __forceinline__ double exp_neg_term(double d, const double* tab) {
@@ -80,8 +79,7 @@ __device__ __forceinline__ double exp_neg_term(double d, const double* tab) {
   q = fma(q, r, 0.5);
   q = fma(q, r, 1.0);
   q = fma(q, r, 1.0);
-  const double v = tab[k & 63] * q;
-  return __hiloint2double(__double2hiint(v) + ((k >> 6) << 20), __double2loint(v));
+  return ldexp(tab[k & 63] * q, k >> 6);
 }
 
 // ------------------------------------------------------- value histograms

@@ -40,11 +40,6 @@ namespace plh {
 
 constexpr int kU = 8;             // 16-byte loads per thread per chunk
 constexpr int kHB = 1024;         // histogram bins
-// k_sample_chunks keeps its histogram's bin b at hpad(b): one pad word
-// after every 16 bins, so 64 lanes reading 16 consecutive bins each
-// (stride 17 words) hit distinct LDS banks.
-constexpr int kHBPad = kHB + kHB / 16;
-__device__ __forceinline__ int hpad(int b) { return b + (b >> 4); }
 constexpr int kCandCap = 8192;    // candidates one row gathers
 constexpr int kCapChunk = 1024;   // candidate slots per chunk, at most
 constexpr int kMaxChunks = 64;    // chunks per row, at most (V <= 262144)
@@ -181,13 +176,17 @@ struct ChunkSmem {
   int ctl[8];
   uint64_t ctlu[4];
   double exp_tab[kWaves][64];  // one copy per wave
-  uint32_t hcnt[kHBPad];  // value histogram, bin b at hpad(b)
+  alignas(16) uint32_t hcnt[kHB];  // value histogram (read 16 bins per lane, 16 bytes at a time)
   uint32_t bitmap[Geo<float>::kChunk / 32];
   double pz[kWaves][kPenPerWave];
   int pt[kWaves][kPenPerWave];
   // candidates staged on their way to the workspace: the raw value and
-  // (lane << 5 | register slot) of the wave that holds it
-  StageRaw sraw[kCapChunk];
+  // its token index (kCodePen for a penalised token written directly);
+  // float inputs keep both in one 8-byte pair, (float bits, index)
+  union {
+    StageRaw sraw[kCapChunk];
+    uint2 spair[kCapChunk];
+  };
   uint32_t scode[kCapChunk];
   int cand_n;
 };
@@ -200,6 +199,47 @@ template <typename TIn>
 __device__ __forceinline__ int slot_q(int e) {
   using G = Geo<TIn>;
   return wave() * G::kSeg + (e / G::kVW) * G::kSpan + lane() * G::kVW + (e % G::kVW);
+}
+
+// Maxima and the running top two of the register tokens in their input
+// precision.  On float, fmax and fmin make the compiler quiet a possible
+// signalling NaN in every loaded value first, one more instruction per
+// token and pass; NaN is outside the input domain, so float tokens go to
+// v_max3_f32, v_max_f32 and v_med3_f32 directly.
+template <typename TIn>
+__device__ __forceinline__ TIn in_max3(TIn a, TIn b, TIn c) {
+  if constexpr (sizeof(TIn) == 4) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+  } else {
+    return fmax(fmax(a, b), c);
+  }
+}
+// (m1, m2): the largest two values seen (m1 >= m2), then x
+template <typename TIn>
+__device__ __forceinline__ void in_top2(TIn& m1, TIn& m2, TIn x) {
+  if constexpr (sizeof(TIn) == 4) {
+    asm("v_med3_f32 %0, %1, %2, %3" : "=v"(m2) : "v"(m1), "v"(m2), "v"(x));
+    asm("v_max_f32 %0, %1, %2" : "=v"(m1) : "v"(m1), "v"(x));
+  } else {
+    m2 = fmax(m2, fmin(m1, x));
+    m1 = fmax(m1, x);
+  }
+}
+
+// acc plus the number of lanes below the calling one whose bit is set in m
+__device__ __forceinline__ int mbcnt(uint64_t m, int acc) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, (uint32_t)acc));
+}
+
+// Wave minimum / maximum of float64 values that are all floats when fl
+// (uniform) holds: then reduced in float, half the DPP moves and compares.
+__device__ __forceinline__ double wave_min_fd(double v, bool fl) {
+  return fl ? (double)wave_min((float)v) : wave_min(v);
+}
+__device__ __forceinline__ double wave_max_fd(double v, bool fl) {
+  return fl ? (double)wave_max((float)v) : wave_max(v);
 }
 
 template <typename TIn, bool VEC>
@@ -345,30 +385,28 @@ struct InAffine {
   Affine af;
   __device__ __forceinline__ explicit InAffine(const Affine& a) : af(a) {}
   __device__ __forceinline__ int bin(TIn x) const { return af.bin(x); }
-  // bin(x) for finite x, af.nb for -inf
-  __device__ __forceinline__ int bin_or_discard(TIn x) const { return x > -INFINITY ? af.bin(x) : af.nb; }
   __device__ __forceinline__ double lo() const { return af.lo; }
   __device__ __forceinline__ double scale() const { return af.scale; }
 };
 template <>
 struct InAffine<float> {
-  float lo_f, scale_f;
+  float lo_f, scale_f, off_f;
   int nb;
   __device__ __forceinline__ explicit InAffine(const Affine& a) : nb(a.nb) {
     lo_f = __double2float_rd(a.lo);
     scale_f = (float)a.scale;
     if (!(scale_f < INFINITY)) scale_f = 0.0f;
+    off_f = -lo_f * scale_f;
   }
-  // finite x >= lo_f: the scaled offset is >= 0 and the median clamps it
-  // to [0, nb - 1]
+  // finite x >= lo_f: x * scale - lo * scale in one fma, clamped to
+  // [0, nb - 1] by the median.  Rounding moves a bin edge by ~2^-24 of
+  // |lo| * scale bins: well inside the threshold's 0.01-bin margin for
+  // logits of ordinary range.  Far outside it, a bin holds a few tokens
+  // too many or too few; the candidate test (x >= theta) and the bound
+  // (theta) stay exact, so that changes only how many candidates a chunk
+  // keeps.
   __device__ __forceinline__ int bin(float x) const {
-    return (int)__builtin_amdgcn_fmed3f((x - lo_f) * scale_f, 0.0f, (float)(nb - 1));
-  }
-  // bin(x) for finite x, nb for -inf, without a branch: x >= lo_f makes
-  // the scaled offset >= 0, and the median clamps it to [0, nb - 1]
-  __device__ __forceinline__ int bin_or_discard(float x) const {
-    const float t = __builtin_amdgcn_fmed3f((x - lo_f) * scale_f, 0.0f, (float)(nb - 1));
-    return x > -INFINITY ? (int)t : nb;
+    return (int)__builtin_amdgcn_fmed3f(fmaf(x, scale_f, off_f), 0.0f, (float)(nb - 1));
   }
   __device__ __forceinline__ double lo() const { return (double)lo_f; }
   __device__ __forceinline__ double scale() const { return (double)scale_f; }
@@ -386,25 +424,35 @@ __device__ __forceinline__ TIn in_threshold(double theta) {
 // Every wave walks the kHB bins of a count histogram from the highest down
 // on its own (no barrier): the bin where the running count first reaches
 // target, -1 when the total stays below it.  Exactly one bin takes the
-// running count from below target to target or more.
+// running count from below target to target or more.  Two levels: lane l
+// sums the 16 bins of group 63 - l (four 16-byte reads) and a wave scan
+// finds the group; the 16 lanes of each row then take one bin of that
+// group each, highest first, and a row scan finds the bin.
 __device__ __forceinline__ int hist_reach_desc(const uint32_t* h, uint32_t target) {
-  constexpr int PL = kHB / kWave;  // lane l walks bins kHB-1-l*PL ... downwards
-  uint32_t c[PL], sum = 0;
+  constexpr int PL = kHB / kWave;
+  static_assert(PL == 16, "one 16-lane row per group");
+  const int grp = kWave - 1 - lane();
+  const uint4* hv = reinterpret_cast<const uint4*>(h + grp * PL);
+  uint32_t sum = 0;
 #pragma unroll
-  for (int i = 0; i < PL; ++i) {
-    c[i] = h[hpad(kHB - 1 - (lane() * PL + i))];
-    sum += c[i];
+  for (int i = 0; i < PL / 4; ++i) {
+    const uint4 q = hv[i];
+    sum += (q.x + q.y) + (q.z + q.w);
   }
   const uint32_t inc = wave_scan_incl(sum, 0u, OpAdd{});
-  uint32_t run = inc - sum;
-  int d = -1;
-#pragma unroll
-  for (int i = 0; i < PL; ++i) {
-    if (d < 0 && run < target && run + c[i] >= target) d = kHB - 1 - (lane() * PL + i);
-    run += c[i];
-  }
-  const uint64_t hb = __ballot(d >= 0);
-  return hb == 0ull ? -1 : lane_value(d, __builtin_ctzll(hb));
+  const uint64_t cross = __ballot(inc - sum < target && inc >= target);
+  if (cross == 0ull) return -1;
+  const int lc = __builtin_ctzll(cross);
+  const uint32_t above = lane_value(inc - sum, lc);
+  const int base = (kWave - 1 - lc) * PL + PL - 1;  // the group's highest bin
+  const int j = lane() & (PL - 1);
+  uint32_t r = h[base - j];
+  r += dpp<kDppRowShr1, 0xf>(0u, r);
+  r += dpp<kDppRowShr2, 0xf>(0u, r);
+  r += dpp<kDppRowShr4, 0xf>(0u, r);
+  r += dpp<kDppRowShr8, 0xf>(0u, r);
+  const uint64_t hit = __ballot(above + r >= target) & 0xffffull;
+  return base - __builtin_ctzll(hit);
 }
 
 // Candidates of one chunk: every finite z >= theta, with theta below the
@@ -421,65 +469,67 @@ __device__ __forceinline__ int hist_reach_desc(const uint32_t* h, uint32_t targe
 // theta is the lower edge of the histogram bin holding the target-th
 // largest (cm.hcnt is zeroed at kernel start; every wave finds that bin on
 // its own), so every token left out is below theta, which serves as the
-// chunk's bound on them.  The passes over
-// the register tokens compare in the input precision (exact: a float
-// converts to float64 exactly).  Each wave writes its candidates to a range
-// of the chunk's slots and its part: the chunk's largest z, theta, the end
-// of its slots.  lmax is the calling thread's largest z.
+// chunk's bound on them.  The passes over the register tokens compare in
+// the input precision (exact: a float converts to float64 exactly).  Each
+// wave counts its candidates with one ballot per register slot (a scalar
+// popcount), reserves a range of the chunk's slots with one LDS atomic and
+// places them with mbcnt, so consecutive candidates of a slot take
+// consecutive slots; then it writes its part: the chunk's largest z,
+// theta, the end of its slots.
+//   lmax: the calling thread's largest z; wmax: its wave's (uniform);
+//   m2: the thread's second-largest register token (when !by_max);
+//   fl: every token of the wave is a float (no float64 pool entries).
 template <typename TIn>
-__device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax, const SampleArgs& a,
-                                                 const RowParams& rp, int g, int c0, int flags, WavePart* wp,
-                                                 ChunkSmem& cm) {
-  constexpr int kEpt = Geo<TIn>::kEpt;
+__device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax, double wmax, TIn m2, bool by_max,
+                                                 uint64_t target, bool fl, const SampleArgs& a, int g, int c0,
+                                                 int flags, WavePart* wp, ChunkSmem& cm) {
+  using G = Geo<TIn>;
+  constexpr int kEpt = G::kEpt;
   const int capc = a.ws.capc;
-  // top-p rows keep as many as the slots allow, less a margin for the
-  // histogram bin that straddles the threshold
-  const uint64_t keep = (uint64_t)(capc - capc / 16);
-  const uint64_t target = rp.topk ? min((uint64_t)rp.top_k, keep) : keep;
-  const bool by_max = rp.topk && target <= (uint64_t)kThreads;
-  double lo = INFINITY, hi = lmax;
-  if (by_max) {
-    if (lmax > -INFINITY) lo = lmax;
-    block_minmax(&lo, &hi, cm.redd);
-  } else {
-    TIn m1 = (TIn)(-INFINITY), m2 = (TIn)(-INFINITY);
-    tk.new_pass();
-#pragma unroll
-    for (int e = 0; e < kEpt; ++e) {
-      const TIn x = tk.rv(e);
-      m2 = fmax(m2, fmin(m1, x));
-      m1 = fmax(m1, x);
+  double lo = INFINITY, hi = wmax;
+  if (by_max) {  // the smallest per-thread maximum and the chunk's max: one barrier round
+    const double l1 = wave_min_fd(lmax > -INFINITY ? lmax : INFINITY, fl);
+    if (lane() == 0) {
+      cm.redd[wave()] = l1;
+      cm.redd[kWaves + wave()] = hi;
     }
-    // one barrier round: min of the finite m2, their count, max of lmax
-    double l2 = m2 > (TIn)(-INFINITY) ? (double)m2 : INFINITY;
-    int n2 = m2 > (TIn)(-INFINITY) ? 1 : 0;
-    l2 = wave_min(l2);
-    hi = wave_max(hi);
-    n2 = wave_sum(n2);
+    wg_barrier();
+    lo = cm.redd[0];
+    hi = cm.redd[kWaves];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+      lo = fmin(lo, cm.redd[w]);
+      hi = fmax(hi, cm.redd[kWaves + w]);
+    }
+  } else {
+    // one barrier round: min of the finite m2, their count, max of wmax
+    const TIn inf = (TIn)INFINITY;
+    const double l2 = (double)wave_min(m2 > -inf ? m2 : inf);
+    const int n2 = (int)__popcll(__ballot(m2 > -inf));
     if (lane() == 0) {
       cm.redd[wave()] = l2;
       cm.redd[kWaves + wave()] = hi;
       cm.redi[wave()] = n2;
     }
     wg_barrier();
-    l2 = cm.redd[0];
+    double l2b = cm.redd[0];
     hi = cm.redd[kWaves];
-    n2 = cm.redi[0];
+    int n2b = cm.redi[0];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) {
-      l2 = fmin(l2, cm.redd[w]);
+      l2b = fmin(l2b, cm.redd[w]);
       hi = fmax(hi, cm.redd[kWaves + w]);
-      n2 += cm.redi[w];
+      n2b += cm.redi[w];
     }
-    if (2 * (uint64_t)uniform(n2) >= target) {
-      lo = l2;
+    if (2 * (uint64_t)uniform(n2b) >= target) {
+      lo = l2b;
     } else {  // few finite tokens: L is the smallest one
-      TIn m = (TIn)INFINITY;
+      TIn m = inf;
       tk.new_pass();
 #pragma unroll
       for (int e = 0; e < kEpt; ++e) {
         const TIn x = tk.rv(e);
-        m = fmin(m, x > (TIn)(-INFINITY) ? x : (TIn)INFINITY);
+        m = fmin(m, x > -inf ? x : inf);
       }
       lo = (double)m;
       for (int i = 0; i < tk.np; ++i) {
@@ -499,21 +549,23 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
     const InAffine<TIn> rf(af);
     double tlo = af.lo, tscale = af.scale;
     if (by_max) {
-      if (lmax > -INFINITY) lds_add(&cm.hcnt[hpad(af.bin(lmax))], 1u);
+      if (lmax > -INFINITY) lds_add(&cm.hcnt[af.bin(lmax)], 1u);
     } else {
       tlo = rf.lo();
       tscale = rf.scale();
       const Affine pf{tlo, tscale, kHB};  // the same bins in float64, for the penalised tokens
       const TIn lin = in_threshold<TIn>(lo);
+      uint32_t one = 1u;  // kept in a register, not rematerialised for every slot
+      asm volatile("" : "+v"(one));
       tk.new_pass();
 #pragma unroll
       for (int e = 0; e < kEpt; ++e) {
         const TIn x = tk.rv(e);
-        if (x >= lin) lds_add(&cm.hcnt[hpad(rf.bin(x))], 1u);
+        if (x >= lin) lds_add(&cm.hcnt[rf.bin(x)], one);
       }
       for (int i = 0; i < tk.np; ++i) {
         const double z = tk.pen_z(cm, i);
-        if (z > -INFINITY && z >= lo) lds_add(&cm.hcnt[hpad(pf.bin(z))], 1u);
+        if (z > -INFINITY && z >= lo) lds_add(&cm.hcnt[pf.bin(z)], 1u);
       }
     }
     wg_barrier();
@@ -524,22 +576,20 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
   }
   theta = uniform(theta);
   const TIn tin = in_threshold<TIn>(theta);
-  int rcnt = 0;  // register tokens kept
+  // lane 0 holds the most pool entries (entry i is on lane i mod 64)
+  const int npw = uniform(tk.np);
+  int wtot = 0;
   tk.new_pass();
 #pragma unroll
-  for (int e = 0; e < kEpt; ++e) rcnt += tk.rv(e) >= tin ? 1 : 0;
-  uint32_t qm = 0;  // penalised tokens kept
-  for (int i = 0; i < tk.np; ++i) {
-    const double z = tk.pen_z(cm, i);
-    if (z > -INFINITY && z >= theta) qm |= 1u << i;
+  for (int e = 0; e < kEpt; ++e) wtot += (int)__popcll(__ballot(tk.rv(e) >= tin));
+  for (int i = 0; i < npw; ++i) {
+    const double z = i < tk.np ? tk.pen_z(cm, i) : -INFINITY;
+    wtot += (int)__popcll(__ballot(z > -INFINITY && z >= theta));
   }
   // one LDS reservation per wave (cm.cand_n was reset before the barriers above)
-  const int cnt = rcnt + __popc(qm);
-  const int incl = wave_scan_incl(cnt, 0, OpAdd{});
-  const int wtot = lane_value(incl, kWave - 1);
   int base = 0;
-  if (lane() == kWave - 1) base = lds_fetch_add(&cm.cand_n, incl);
-  base = lane_value(base, kWave - 1);
+  if (lane() == 0) base = lds_fetch_add(&cm.cand_n, wtot);
+  base = lane_value(base, 0);
   // the wave's candidates go to its slots [base, base + wtot) in LDS first,
   // then to the workspace with consecutive lanes on consecutive slots; a
   // wave whose slots would run past capc makes the chunk incomplete
@@ -548,37 +598,57 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
     flags |= kChunkIncomplete;
     wend = base;
   } else {
-    // register tokens: the raw value and (lane, slot) go to LDS; the
+    // register tokens: the raw value and the token index go to LDS; the
     // penalised ones (few) straight to the workspace with their float64
     // value and token id
-    int slot = base + incl - cnt;
     double* cz = a.ws.cz + (size_t)g * capc;
     int32_t* ci = a.ws.ci + (size_t)g * capc;
-    const uint32_t code0 = (uint32_t)lane() << 5;
+    const int idx0 = c0 + slot_q<TIn>(0);
+    int pos = base;
     tk.new_pass();
 #pragma unroll
     for (int e = 0; e < kEpt; ++e) {
-      if (tk.rv(e) >= tin) {
-        cm.sraw[slot] = tk.rv(e);
-        cm.scode[slot] = code0 | (uint32_t)e;
-        ++slot;
+      const TIn x = tk.rv(e);
+      const bool keep = x >= tin;
+      const uint64_t m = __ballot(keep);
+      if (keep) {
+        const int s = pos + mbcnt(m, 0);
+        const uint32_t code = (uint32_t)(idx0 + (e / G::kVW) * G::kSpan + (e % G::kVW));
+        if constexpr (sizeof(TIn) == 4) {
+          cm.spair[s] = make_uint2(__float_as_uint(x), code);
+        } else {
+          cm.sraw[s] = x;
+          cm.scode[s] = code;
+        }
       }
+      pos += (int)__popcll(m);
     }
-    for (int i = 0; i < tk.np; ++i) {
-      if ((qm >> i) & 1u) {
-        cm.scode[slot] = kCodePen;
-        cz[slot] = tk.pen_z(cm, i);
-        ci[slot] = tk.pen_tok(cm, i);
-        ++slot;
+    for (int i = 0; i < npw; ++i) {
+      const double z = i < tk.np ? tk.pen_z(cm, i) : -INFINITY;
+      const bool keep = z > -INFINITY && z >= theta;
+      const uint64_t m = __ballot(keep);
+      if (keep) {
+        const int s = pos + mbcnt(m, 0);
+        if constexpr (sizeof(TIn) == 4) cm.spair[s].y = kCodePen;
+        else cm.scode[s] = kCodePen;
+        cz[s] = z;
+        ci[s] = tk.pen_tok(cm, i);
       }
+      pos += (int)__popcll(m);
     }
-    using G = Geo<TIn>;
     for (int i = base + lane(); i < wend; i += kWave) {
-      const uint32_t code = cm.scode[i];
-      if (code != kCodePen) {
-        const int ln = (int)(code >> 5), e = (int)(code & 31u);
-        cz[i] = sizeof(TIn) == 4 ? (double)cm.sraw[i].f : cm.sraw[i].d;
-        ci[i] = c0 + wave() * G::kSeg + (e / G::kVW) * G::kSpan + ln * G::kVW + (e % G::kVW);
+      if constexpr (sizeof(TIn) == 4) {
+        const uint2 pr = cm.spair[i];
+        if (pr.y != kCodePen) {
+          cz[i] = (double)__uint_as_float(pr.x);
+          ci[i] = (int32_t)pr.y;
+        }
+      } else {
+        const uint32_t code = cm.scode[i];
+        if (code != kCodePen) {
+          cz[i] = cm.sraw[i].d;
+          ci[i] = (int32_t)code;
+        }
       }
     }
   }
@@ -611,7 +681,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   load_chunk<TIn, VEC>(x, a.V, c0, tk.v);
   const bool cands = rp.topk || (rp.topp && !(NUC && rp.nucleus));
   if (cands) {  // ordered before use by the first barrier of chunk_candidates
-    for (int b = threadIdx.x; b < kHBPad; b += kThreads) cm.hcnt[b] = 0u;
+    for (int b = threadIdx.x; b < kHB; b += kThreads) cm.hcnt[b] = 0u;
     if (threadIdx.x == 0) cm.cand_n = 0;
   }
   int flags = 0;
@@ -645,16 +715,31 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     return;
   }
   const double* tab = cm.exp_tab[wave()];
-  init_exp_table_wave(cm.exp_tab[wave()]);
-  TIn lm = (TIn)(-INFINITY);
+  if (!rp.topk) init_exp_table_wave(cm.exp_tab[wave()]);
+  // top-p rows keep as many candidates as the slots allow, less a margin
+  // for the histogram bin that straddles the threshold
+  const int capc = a.ws.capc;
+  const uint64_t keep = (uint64_t)(capc - capc / 16);
+  const uint64_t target = rp.topk ? min((uint64_t)rp.top_k, keep) : keep;
+  const bool by_max = rp.topk && target <= (uint64_t)kThreads;
+  // the thread's largest register token, and its second largest when the
+  // chunk's threshold needs a lower edge, in one pass
+  TIn m1 = (TIn)(-INFINITY), m2 = (TIn)(-INFINITY);
   tk.new_pass();
+  if (cands && !by_max) {
 #pragma unroll
-  for (int e = 0; e < G::kEpt; ++e) {
-    lm = fmax(lm, tk.rv(e));
+    for (int e = 0; e < G::kEpt; ++e) in_top2(m1, m2, tk.rv(e));
+  } else {
+#pragma unroll
+    for (int e = 0; e < G::kEpt; e += 2) m1 = in_max3(m1, tk.rv(e), tk.rv(e + 1));
   }
-  double lmax = (double)lm;
+  double lmax = (double)m1;
   for (int i = 0; i < tk.np; ++i) lmax = fmax(lmax, tk.pen_z(cm, i));
-  if (cands) chunk_candidates<TIn>(tk, lmax, a, rp, g, c0, flags, wp, cm);
+  // lane 0 holds the most pool entries: none there means the wave's
+  // tokens are all in the registers, in the input precision
+  const bool fl = sizeof(TIn) == 4 && uniform(tk.np) == 0;
+  const double wmax = uniform(wave_max_fd(lmax, fl));
+  if (cands) chunk_candidates<TIn>(tk, lmax, wmax, m2, by_max, target, fl, a, g, c0, flags, wp, cm);
   else if (lane() == 0) wp->flags = flags;
   if (NUC && rp.nucleus && g == row * C)  // the row's count histogram, filled by k_nuc_hist
     for (int b = threadIdx.x; b < kNucBins; b += kThreads) a.ws.ncnt[(size_t)row * kNucBins + b] = 0u;
@@ -672,16 +757,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       if (z > -INFINITY) zmn = fmin(zmn, z);
     }
     zmn = wave_min(zmn);
-    const double zmx = wave_max(lmax);
     if (lane() == 0) {
       wp->umax = zmn;  // the nucleus kernels' lower range edge
-      wp->zmax = zmx;
+      wp->zmax = wmax;
     }
   }
   if (!rp.topk) {  // the full-vocabulary normaliser (sampling.py:79-81)
     // y = z / T is monotone in z, so the segment's max y is y(max z)
     const YScale ys{rp.T, 1.0 / rp.T};
-    const double m = uniform(ys(wave_max(lmax)));
+    const double m = uniform(ys(wmax));
     double s = 0.0;
     if (m > -INFINITY) {
       tk.new_pass();
