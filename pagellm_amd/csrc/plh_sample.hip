@@ -950,32 +950,55 @@ struct SelOut {
   int idx;
 };
 
+// Bounds on the active set known before a selection: every active key lies
+// in [lo, hi], and n bounds the active count from above (exact when the
+// selection is a top-k one: its n < target test needs the count).
+struct KeySpan {
+  uint64_t lo, hi, n;
+};
+
 // The order key of slot q is keyf(rc.v[q]), non-decreasing in rc.v[q], so
-// the key range of the active set comes from the range of the values.
+// the key range of the active set comes from the range of the values: one
+// cross-wave combine, skipped when the caller passes a KeySpan (known).  The rank
+// list reads its entry count from the list itself, so an upper bound n
+// only decides whether a histogram level runs first.
 template <bool MASS, class KeyF>
 __device__ __forceinline__ SelOut select_desc(uint32_t act, const RegCands& rc, const KeyF& keyf, uint64_t target,
-                                              int V, RankList& rl, FastSmem& fs, XWave& xw, int& hgen) {
+                                              int V, RankList& rl, FastSmem& fs, XWave& xw, int& hgen,
+                                              bool known = false, KeySpan span = KeySpan{0, 0, 0}) {
   auto key = [&](int q) -> uint64_t { return keyf(rc.v[q]); };
-  double vlo = INFINITY, vhi = -INFINITY;
-#pragma unroll
-  for (int q = 0; q < kPerT; ++q)
-    if ((act >> q) & 1u) {
-      vlo = fmin(vlo, rc.v[q]);
-      vhi = fmax(vhi, rc.v[q]);
-    }
   {
-    const auto s = xw.post(bits_of(wave_min(vlo)), bits_of(wave_max(vhi)), (uint64_t)wave_sum((uint32_t)__popc(act)));
-    vlo = dbl_of(s[0][0]);
-    vhi = dbl_of(s[1][0]);
-    uint64_t n = s[2][0];
+    uint64_t lo, hi, n;
+    if (known) {
+      // the barrier the combine below would have given: the kernel zeroes
+      // the first histogram and the rank lists at its start and orders
+      // that before their first use with the row's first barrier, which
+      // for a top-p-only row is this one
+      wg_barrier();
+      lo = span.lo;
+      hi = span.hi;
+      n = span.n;
+    } else {
+      double vlo = INFINITY, vhi = -INFINITY;
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) {
-      vlo = fmin(vlo, dbl_of(s[0][w]));
-      vhi = fmax(vhi, dbl_of(s[1][w]));
-      n += s[2][w];
+      for (int q = 0; q < kPerT; ++q)
+        if ((act >> q) & 1u) {
+          vlo = fmin(vlo, rc.v[q]);
+          vhi = fmax(vhi, rc.v[q]);
+        }
+      const auto s = xw.post(bits_of(wave_min(vlo)), bits_of(wave_max(vhi)), (uint64_t)wave_sum((uint32_t)__popc(act)));
+      vlo = dbl_of(s[0][0]);
+      vhi = dbl_of(s[1][0]);
+      n = s[2][0];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) {
+        vlo = fmin(vlo, dbl_of(s[0][w]));
+        vhi = fmax(vhi, dbl_of(s[1][w]));
+        n += s[2][w];
+      }
+      lo = uniform(keyf(vlo));
+      hi = uniform(keyf(vhi));
     }
-    uint64_t lo = uniform(keyf(vlo));
-    uint64_t hi = uniform(keyf(vhi));
     if (n == 0 || (!MASS && n < target)) return SelOut{false, false, 0, 0};
     target = uniform(target);
     uint32_t cnt = (uint32_t)uniform(n);
@@ -1036,7 +1059,7 @@ __device__ __forceinline__ SelOut select_desc(uint32_t act, const RegCands& rc, 
     // lane i of every wave holds entry i; wave w compares it with entries
     // j in [8w, 8w + 8) (LDS broadcast reads) and adds its counts to the
     // entry's totals
-    const int m = uniform((int)cnt);
+    const int m = uniform(rl.n);
     const int ln = lane();
     uint64_t k = 0ull, w = 0ull;
     int ix = INT_MAX;
@@ -1154,6 +1177,7 @@ __device__ __forceinline__ int draw_kept(const RegCands& rc, int V, double u, Fa
 struct PartSum {
   int flags;
   double umax, zmax;
+  double umin;  // the smallest chunk threshold: every candidate is >= it
   ArgMax best;
 };
 
@@ -1163,7 +1187,7 @@ __device__ __forceinline__ PartSum scan_parts(const SampleArgs& a, int row, bool
   int* wc = fs.wcnt[wave()];
   if (cands) wc[lane()] = 0;
   int fl = 0;
-  double um = -INFINITY, zm = -INFINITY;
+  double um = -INFINITY, zm = -INFINITY, un = INFINITY;
   ArgMax best{-INFINITY, INT_MAX};
   for (int j = lane(); j < P; j += kWave) {
     const WavePart& p = pp[j];
@@ -1171,6 +1195,7 @@ __device__ __forceinline__ PartSum scan_parts(const SampleArgs& a, int row, bool
     if (greedy) best = argmax_merge(best, ArgMax{p.best_z, p.best_idx});
     if (cands) {
       um = fmax(um, p.umax);
+      un = fmin(un, p.umax);
       zm = fmax(zm, p.zmax);
       lds_max(&wc[j / kWaves], p.end);  // a chunk's count: the largest end of its waves
     }
@@ -1178,6 +1203,7 @@ __device__ __forceinline__ PartSum scan_parts(const SampleArgs& a, int row, bool
   PartSum r;
   r.flags = uniform(wave_max(fl));
   r.umax = uniform(wave_max(um));
+  r.umin = cands ? uniform(wave_min(un)) : INFINITY;
   r.zmax = uniform(wave_max(zm));
   r.best = greedy ? wave_argmax(best) : best;
   return r;
@@ -1342,14 +1368,24 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, RegCands& r
     const int i = q * kThreads + (int)threadIdx.x;
     if (i < slots && (i & (capc - 1)) < wc[i >> csh]) rc.valid |= 1u << q;
   }
+  // the row's candidate count, by every wave from its copy of the counts
+  // (computed where needed, to keep it out of the registers in between)
+  auto count_cands = [&]() -> uint64_t {
+    int nc = 0;
+    for (int c = lane(); c < a.ws.C; c += kWave) nc += wc[c];
+    return (uint64_t)uniform(wave_sum(nc));
+  };
   const double T = rp.T;
   auto yexact = [&](double z) -> double { return T == 1.0 ? z : z / T; };
 
   // ---- top-k: k-th largest with multiplicity, keep y >= kth_y (:76-78)
   double z_lo = -INFINITY;
   if (TOPK) {
+    // every candidate lies in [the smallest chunk threshold, the row max]
+    const KeySpan ks{key_of(ps.umin), key_of(ps.zmax), count_cands()};
+    const bool known = ps.umin > -INFINITY && ps.umin <= ps.zmax;
     const SelOut r = select_desc<false>(rc.valid, rc, [](double z) { return key_of(z); }, (uint64_t)rp.top_k,
-                                        V, fs.rl[0], fs, xw, hgen);
+                                        V, fs.rl[0], fs, xw, hgen, known, ks);
     if (!r.found) return FastOut{V - 1, true, 0.0};
     const double kth_z = val_of_key(r.key);
     const double kth_y = yexact(kth_z);
@@ -1366,19 +1402,32 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, RegCands& r
   const YScale ys{T, 1.0 / T};
   const double ymax = ys(ps.zmax);
   double s = 0.0;
+  uint32_t nkept = 0;
 #pragma unroll
   for (int q = 0; q < kPerT; ++q) {
     const double z = rc.v[q];
-    const double e = (((rc.valid >> q) & 1u) && z >= z_lo) ? fast_exp_neg(ys(z) - ymax, tab) : 0.0;
+    const bool kept = ((rc.valid >> q) & 1u) && z >= z_lo;
+    const double e = kept ? fast_exp_neg(ys(z) - ymax, tab) : 0.0;
+    nkept += kept ? 1u : 0u;
     rc.v[q] = e;
     s += e;
   }
   double S;
+  uint64_t nk = 0;  // the top-p selection's active count, bounded above
   if (TOPK) {
-    S = xw_sum(xw, s);
+    // the normaliser (waves left to right, as xw_sum) and the kept count
+    const auto sk = xw.post(bits_of(wave_sum(s)), (uint64_t)wave_sum(nkept), 0);
+    S = 0.0;
+    nk = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      S += dbl_of(sk[0][w]);
+      nk += sk[1][w];
+    }
   } else {
     double ms[kSegPerLane], lex;
     S = seg_norm(sg, tab, ms, &lex).S;
+    nk = count_cands();
   }
   const double invS = 1.0 / S;
   uint32_t pos = 0;
@@ -1392,8 +1441,17 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, RegCands& r
   // ---- top-p: first token (p desc, index asc) whose inclusive mass reaches
   // top_p (:82-90)
   if (rp.topp) {
+    // every probability lies in [p(smallest chunk threshold), 1 / S] up to
+    // rounding: the row max's exp argument ys(z) - ymax may be contracted
+    // to an fma and come out a rounding residual above 0, so its e can be
+    // 1 + 2^-52, and the exp is monotone only up to an ulp.  Both ends get
+    // 2^32 ulps of slack (a relative 2^-20).  The count bounds the active
+    // set from above (underflows to 0 drop out).
+    constexpr uint64_t kSlack = 1ull << 32;
+    const uint64_t plo = pkey_of(fast_exp_neg(ys(ps.umin) - ymax, tab) * invS);
+    const KeySpan ps_span{plo > kSlack ? plo - kSlack : 0ull, pkey_of(invS) + kSlack, uniform(nk)};
     const SelOut r = select_desc<true>(pos, rc, [](double p) { return pkey_of(p); }, topp_target(rp.top_p), V,
-                                       fs.rl[1], fs, xw, hgen);
+                                       fs.rl[1], fs, xw, hgen, true, ps_span);
     if (r.giveup) return FastOut{V - 1, true, TOPK ? 0.0 : S};
     if (r.found) {
 #pragma unroll
