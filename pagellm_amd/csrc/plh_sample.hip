@@ -699,12 +699,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     // max, then the lowest slot holding it
     TIn m = (TIn)(-INFINITY);
 #pragma unroll
-    for (int e = 0; e < G::kEpt; ++e) m = fmax(m, tk.v[e / G::kVW][e % G::kVW]);
-    uint32_t eq = 0u;
+    for (int e = 0; e < G::kEpt; e += 2) m = in_max3(m, tk.rv(e), tk.rv(e + 1));
+    int first = G::kEpt;  // the lowest register slot holding m
 #pragma unroll
-    for (int e = 0; e < G::kEpt; ++e) eq |= tk.v[e / G::kVW][e % G::kVW] == m ? 1u << e : 0u;
+    for (int e = G::kEpt - 1; e >= 0; --e) first = tk.rv(e) == m ? e : first;
     ArgMax best{-INFINITY, INT_MAX};
-    if (eq != 0u) best = ArgMax{(double)m, c0 + slot_q<TIn>(__builtin_ctz(eq))};
+    if (first < G::kEpt) best = ArgMax{(double)m, c0 + slot_q<TIn>(first)};
     for (int i = 0; i < tk.np; ++i) best = argmax_merge(best, ArgMax{tk.pen_z(cm, i), tk.pen_tok(cm, i)});
     best = wave_argmax(best);
     if (lane() == 0) {
@@ -1589,10 +1589,11 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
 struct NucBin {
   float lo, scale;
   __device__ __forceinline__ explicit NucBin(const NucRow& nr) : lo((float)nr.zlo), scale((float)nr.scale) {}
-  __device__ __forceinline__ int operator()(double z) const {
-    const float t = ((float)z - lo) * scale;
+  __device__ __forceinline__ int operator()(float zf) const {
+    const float t = (zf - lo) * scale;
     return (int)__builtin_amdgcn_fmed3f(t, 0.0f, (float)(kNucBins - 1));
   }
+  __device__ __forceinline__ int operator()(double z) const { return (*this)((float)z); }
 };
 
 // The calling lane's penalty bits (as chunk_pbits) from the chunk bitmap
@@ -1640,11 +1641,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   }
   wg_barrier();
   const NucBin nb(nr);
+  uint32_t one = 1u;  // kept in a register, not rematerialised for every slot
+  asm volatile("" : "+v"(one));
   tk.new_pass();
 #pragma unroll
   for (int e = 0; e < G::kEpt; ++e) {
     const TIn v = tk.rv(e);
-    if (v > (TIn)(-INFINITY)) lds_add(&nh[nb((double)v)], 1u);
+    if (v > (TIn)(-INFINITY)) lds_add(&nh[nb((float)v)], one);
   }
   for (int i = 0; i < tk.np; ++i) {
     const double z = tk.pen_z(cm, i);
@@ -1821,27 +1824,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   double* sz = stz[wave()];
   StageRaw* cs = cm.sraw + wave() * kNucCandWave;
   uint32_t* cc = cm.scode + wave() * kNucCandWave;
-  const uint64_t below_me = (1ull << lane()) - 1ull;
   double acc = 0.0;  // this lane's share of the side's mass
   int mn = 0, cn = 0;  // staged side tokens and window tokens (the same in every lane)
   auto flush = [&]() {
     for (int i = lane(); i < mn; i += kWave) acc += nuc_p(ys(sz[i]), nr, tab);
     mn = 0;
   };
-  auto take = [&](double z, int idx) {
+  // z: the token's (penalised) logit; zf: z rounded to float, which is
+  // what the bins see (exact for a register token)
+  auto take = [&](double z, float zf, int idx) {
     const bool fin = z > -INFINITY;
-    const int b = nb(z);
+    const int b = nb(zf);
     const bool side = fin && (abv ? b > nr.dhi : b < nr.dlo);
     const bool cand = fin && b >= nr.dlo && b <= nr.dhi;
     const uint64_t ms = __ballot(side);
     if (ms != 0ull) {
-      if (side) sz[mn + __popcll(ms & below_me)] = z;
+      if (side) sz[mbcnt(ms, mn)] = z;
       mn += __popcll(ms);
       if (mn > kNucStage - kWave) flush();
     }
     const uint64_t mc = __ballot(cand);
     if (mc != 0ull) {
-      const int slot = cn + __popcll(mc & below_me);
+      const int slot = mbcnt(mc, cn);
       if (cand && slot < kNucCandWave) {
         cs[slot].d = z;
         cc[slot] = (uint32_t)idx;
@@ -1851,9 +1855,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   };
   tk.new_pass();
 #pragma unroll
-  for (int e = 0; e < G::kEpt; ++e) take((double)tk.rv(e), c0 + slot_q<TIn>(e));
+  for (int e = 0; e < G::kEpt; ++e) take((double)tk.rv(e), (float)tk.rv(e), c0 + slot_q<TIn>(e));
   const int npmax = wave_max(tk.np);
-  for (int i = 0; i < npmax; ++i) take(i < tk.np ? tk.pen_z(cm, i) : -INFINITY, i < tk.np ? tk.pen_tok(cm, i) : 0);
+  for (int i = 0; i < npmax; ++i) {
+    const double z = i < tk.np ? tk.pen_z(cm, i) : -INFINITY;
+    take(z, (float)z, i < tk.np ? tk.pen_tok(cm, i) : 0);
+  }
   flush();
   acc = wave_sum(acc);
   if (lane() == 0) a.ws.nexcl[(size_t)g * kWaves + wave()] = acc;
