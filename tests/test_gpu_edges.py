@@ -49,6 +49,28 @@ def test_random_rows_all_paths(V, dtype):
     _check(x, params, u, ctx, b)
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("V", [8192, 50000])
+def test_tiny_top_p_keeps_the_row_max(V, dtype):
+    """top_p far below the largest probability keeps exactly the row's
+    maximum (sampling.py:82-90), whatever the temperature and penalty.  The
+    row max's exp argument, y(z) - y(zmax), can round to a residual just
+    above 0 when T != 1, which puts its probability an ulp above 1/S; the
+    merge's top-p key range must still hold it."""
+    g = np.random.default_rng(V + 11 * (dtype == np.float64))
+    B = 48
+    x = g.normal(0, 2, (B, V)).astype(dtype)
+    temps = [0.7, 0.9, 1.3, 0.35, 1.0, 2.5]
+    params = [SamplingParams(temperature=temps[b % len(temps)], top_p=1e-9,
+                             repetition_penalty=(1.3, 1.0, 0.8)[b % 3]) for b in range(B)]
+    ctx = [list(g.integers(0, V, 200)) for _ in range(B)]
+    u = g.random(B)
+    ids = sample_batch(x, params, uniforms=u, contexts=ctx)
+    _check(x, params, u, ctx, ids)
+    for b in range(B):
+        assert ids[b] == oracle.sample(x[b], params[b], u[b], ctx[b]), b
+
+
 def test_masked_logits_and_all_ties():
     V = 10000
     x = np.full((4, V), -np.inf, dtype=np.float32)
