@@ -1789,9 +1789,9 @@ constexpr int kNucCandWave = kCapChunk / kWaves;  // window tokens a wave stages
 
 // The window's tokens go to the candidate slots (p and id); the tokens on
 // the row's smaller side of the window (nr.above) have their p summed per
-// segment.  Both are first staged per wave in LDS (a ballot and a bit count
-// per token step), so the exps run densely over the staged tokens instead
-// of in a branch nearly every wave would take.
+// segment.  Both are first staged per wave in LDS (a ballot per token step,
+// each lane's place from mbcnt), so the exps run densely over the staged
+// tokens instead of in a branch nearly every wave would take.
 template <typename TIn, bool VEC>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_nuc_cands(SampleArgs a) {
   using G = Geo<TIn>;
