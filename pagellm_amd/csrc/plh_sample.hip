@@ -216,6 +216,16 @@ __device__ __forceinline__ TIn in_max3(TIn a, TIn b, TIn c) {
     return fmax(fmax(a, b), c);
   }
 }
+template <typename TIn>
+__device__ __forceinline__ TIn in_min3(TIn a, TIn b, TIn c) {
+  if constexpr (sizeof(TIn) == 4) {
+    float r;
+    asm("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+  } else {
+    return fmin(fmin(a, b), c);
+  }
+}
 // (m1, m2): the largest two values seen (m1 >= m2), then x
 template <typename TIn>
 __device__ __forceinline__ void in_top2(TIn& m1, TIn& m2, TIn x) {
@@ -226,6 +236,19 @@ __device__ __forceinline__ void in_top2(TIn& m1, TIn& m2, TIn x) {
     m2 = fmax(m2, fmin(m1, x));
     m1 = fmax(m1, x);
   }
+}
+
+// float64 min / max of values known not to be NaN, without the quieting
+// instruction the compiler adds in front of fmin / fmax
+__device__ __forceinline__ double dmin_raw(double a, double b) {
+  double r;
+  asm("v_min_f64 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ double dmax_raw(double a, double b) {
+  double r;
+  asm("v_max_f64 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
 }
 
 // acc plus the number of lanes below the calling one whose bit is set in m
@@ -498,8 +521,8 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
     hi = cm.redd[kWaves];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) {
-      lo = fmin(lo, cm.redd[w]);
-      hi = fmax(hi, cm.redd[kWaves + w]);
+      lo = dmin_raw(lo, cm.redd[w]);
+      hi = dmax_raw(hi, cm.redd[kWaves + w]);
     }
   } else {
     // one barrier round: min of the finite m2, their count, max of wmax
@@ -517,8 +540,8 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
     int n2b = cm.redi[0];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) {
-      l2b = fmin(l2b, cm.redd[w]);
-      hi = fmax(hi, cm.redd[kWaves + w]);
+      l2b = dmin_raw(l2b, cm.redd[w]);
+      hi = dmax_raw(hi, cm.redd[kWaves + w]);
       n2b += cm.redi[w];
     }
     if (2 * (uint64_t)uniform(n2b) >= target) {
@@ -744,12 +767,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   if (NUC && rp.nucleus && g == row * C)  // the row's count histogram, filled by k_nuc_hist
     for (int b = threadIdx.x; b < kNucBins; b += kThreads) a.ws.ncnt[(size_t)row * kNucBins + b] = 0u;
   if (NUC && rp.nucleus) {  // the range of the row's count histogram
-    TIn lmn = (TIn)INFINITY;
+    // the smallest finite register token (-inf slots count as +inf)
+    const TIn inf = (TIn)INFINITY;
+    TIn lmn = inf;
     tk.new_pass();
 #pragma unroll
-    for (int e = 0; e < G::kEpt; ++e) {
-      const TIn v = tk.rv(e);
-      if (v > (TIn)(-INFINITY)) lmn = fmin(lmn, v);
+    for (int e = 0; e < G::kEpt; e += 2) {
+      const TIn v0 = tk.rv(e), v1 = tk.rv(e + 1);
+      lmn = in_min3(lmn, v0 > -inf ? v0 : inf, v1 > -inf ? v1 : inf);
     }
     double zmn = (double)lmn;
     for (int i = 0; i < tk.np; ++i) {
