@@ -1612,11 +1612,16 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
 // [0, kNucBins - 1], computed in float32 on z rounded to float.  Monotone
 // non-decreasing in z; every kernel that bins a token uses this function.
 struct NucBin {
-  float lo, scale;
-  __device__ __forceinline__ explicit NucBin(const NucRow& nr) : lo((float)nr.zlo), scale((float)nr.scale) {}
+  float lo, scale, top;
+  __device__ __forceinline__ explicit NucBin(const NucRow& nr) : lo((float)nr.zlo), scale((float)nr.scale) {
+    // the clamp's upper end lives in a register: v_med3_f32 takes no
+    // literal, and the compiler would otherwise rebuild it for every token
+    top = (float)(kNucBins - 1);
+    asm volatile("" : "+v"(top));
+  }
   __device__ __forceinline__ int operator()(float zf) const {
     const float t = (zf - lo) * scale;
-    return (int)__builtin_amdgcn_fmed3f(t, 0.0f, (float)(kNucBins - 1));
+    return (int)__builtin_amdgcn_fmed3f(t, 0.0f, top);
   }
   __device__ __forceinline__ int operator()(double z) const { return (*this)((float)z); }
 };
@@ -1855,13 +1860,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     for (int i = lane(); i < mn; i += kWave) acc += nuc_p(ys(sz[i]), nr, tab);
     mn = 0;
   };
+  // the side's bins: above the window, or below it
+  const int slo = abv ? nr.dhi + 1 : 0;
+  const int shi = abv ? kNucBins - 1 : nr.dlo - 1;
   // z: the token's (penalised) logit; zf: z rounded to float, which is
-  // what the bins see (exact for a register token)
+  // what the bins see (exact for a register token).  A -inf token takes
+  // bin -1, outside both ranges; the tests are plain compares, no branches.
   auto take = [&](double z, float zf, int idx) {
-    const bool fin = z > -INFINITY;
-    const int b = nb(zf);
-    const bool side = fin && (abv ? b > nr.dhi : b < nr.dlo);
-    const bool cand = fin && b >= nr.dlo && b <= nr.dhi;
+    const int b = z > -INFINITY ? nb(zf) : -1;
+    const bool side = (b >= slo) & (b <= shi);
+    const bool cand = (b >= nr.dlo) & (b <= nr.dhi);
     const uint64_t ms = __ballot(side);
     if (ms != 0ull) {
       if (side) sz[mbcnt(ms, mn)] = z;
