@@ -351,6 +351,47 @@ def valu_from(workload: str, dirs: list, dst: Path | None = None, shape: tuple |
     return out
 
 
+def valu_kernels_from(workload: str, folder: str, dst: Path | None = None, shape: tuple | None = None) -> dict:
+    """Instructions per token of every sampler kernel of one counter run of
+    the whole batch (`--pmc SQ_INSTS_VALU SQ_INSTS_SALU SQ_INSTS_LDS
+    SQ_WAVES -- python3 bench.py --pmc-probe --workload W`): per kernel
+    (template arguments dropped), the counters averaged over its launches,
+    wave instructions x 64 lanes / the batch's tokens, written to
+    profiles/valu_kernels_<workload>.json."""
+    import csv
+
+    if shape is None:
+        from pagellm_amd import workloads
+        shape = workloads.WORKLOADS[workload]()["logits"].shape
+    B, V = shape
+    per = {}
+    for f in Path(folder).rglob("*counter_collection.csv"):
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] not in VALU_COUNTERS:
+                continue
+            name = r["Kernel_Name"].split("(")[0].split("<")[0].replace("void ", "").replace("plh::", "")
+            if not name.startswith(("k_sample", "k_nuc")):
+                continue
+            d = per.setdefault(name, {}).setdefault(r["Dispatch_Id"], {})
+            d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    if not per:
+        raise SystemExit(f"no sampler kernel counters in {folder}")
+    tokens = B * V
+    kernels = []
+    for name, launches in sorted(per.items()):
+        mean = {c: sum(x.get(c, 0.0) for x in launches.values()) / len(launches) for c in VALU_COUNTERS}
+        kernels.append({"kernel": name, "launches": len(launches), "per_launch": mean,
+                        "valu_per_token": mean["SQ_INSTS_VALU"] * 64 / tokens,
+                        "salu_per_token": mean["SQ_INSTS_SALU"] * 64 / tokens,
+                        "lds_per_token": mean["SQ_INSTS_LDS"] * 64 / tokens})
+    out = {"workload": workload, "tokens_per_launch": tokens,
+           "note": "wave instructions x 64 lanes / the batch's tokens, per kernel launch", "kernels": kernels}
+    dst = dst if dst is not None else ROOT / "profiles" / f"valu_kernels_{workload}.json"
+    dst.write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out))
+    return out
+
+
 MALL_BYTES = 256 << 20  # MI355X Infinity Cache
 ROTATE_BYTES = 2 * MALL_BYTES  # rotating input sets span at least this much, so steps stream from HBM
 
@@ -606,6 +647,8 @@ def main() -> None:
     ap.add_argument("--probe-group", type=int, help="(--pmc-probe) one mixed128k row group, 0-3, repeated")
     ap.add_argument("--valu-from", nargs="+", metavar="DIR",
                     help="counter run folders of --pmc-probe --probe-group 0..3 -> profiles/valu_<workload>.json")
+    ap.add_argument("--valu-kernels-from", metavar="DIR",
+                    help="counter run folder of --pmc-probe (whole batch) -> profiles/valu_kernels_<workload>.json")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the other workloads (zipf32k, zipf152k, char65, spec32k verify)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
@@ -621,6 +664,9 @@ def main() -> None:
         return
     if args.valu_from:
         valu_from(args.workload, args.valu_from)
+        return
+    if args.valu_kernels_from:
+        valu_kernels_from(args.workload, args.valu_kernels_from)
         return
     if args.pmc_probe:
         pmc_probe(args.workload, args.probe_group)
