@@ -1525,7 +1525,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   const bool gather_early = cands && !rp.topk;
   if (gather_early) gather_cands(a, row, rc);
   SegLoad sg;
-  if (!rp.greedy && !rp.topk) {
+  if (!rp.greedy && !rp.topk && !(NUC && rp.nucleus)) {  // nucleus rows only set their bin range here
     load_segs(a, row, (a.V + Geo<TIn>::kSeg - 1) / Geo<TIn>::kSeg, sg);
   }
   const PartSum ps = scan_parts(a, row, rp.greedy, cands, fs);
