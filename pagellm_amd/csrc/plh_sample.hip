@@ -85,6 +85,7 @@ struct FastSmem {
   int wcnt[kWaves][kMaxChunks];       // per wave: candidate count of each chunk
   Hist h[kHBuf];
   uint64_t dspan[kDrawSpanMax];       // the draw's crossing bin, by token offset
+  uint64_t csum[kMaxChunks];          // the draw's per-chunk kept mass
   RankList rl[2];                     // top-k, top-p
   uint32_t segbits[kSegMax / 32];     // penalty bits of a rescanned segment
 };
@@ -684,6 +685,18 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
   }
 }
 
+// Chunk index (row * C + chunk) of a block of the B x C chunk grids.  The
+// hardware deals block ids to the 8 XCDs round robin (block b to XCD b % 8);
+// the blocks of one row all carry the same b % 8, so a row's chunks and its
+// merge (block `row` of the per-row grids) share one XCD's L2.  -1: a
+// padding block (B not a multiple of 8).
+constexpr int kXcds = 8;
+__device__ __forceinline__ int chunk_block(int C, int B) {
+  const int x = (int)blockIdx.x % kXcds, k = (int)blockIdx.x / kXcds;
+  const int row = x + kXcds * (k / C);
+  return row < B ? row * C + k % C : -1;
+}
+
 // One workgroup per 64 KB chunk (rows of any alignment: 16-byte
 // non-temporal loads when the row allows, scalar loads otherwise).  The
 // waves work on their own segments and write their own parts, so greedy and
@@ -695,7 +708,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   using G = Geo<TIn>;
   __shared__ ChunkSmem cm;
   const int C = a.ws.C;
-  const int g = blockIdx.x;
+  const int g = chunk_block(C, a.B);
+  if (g < 0) return;
   const int row = g / C;
   const int c0 = (g - row * C) * G::kChunk;
   const RowParams rp = load_row_params(a, row);
@@ -1496,6 +1510,418 @@ __device__ __forceinline__ FastOut finish_cands(const SampleArgs& a, RegCands& r
   return FastOut{draw_kept(rc, V, rp.u, fs, hgen), false, 0.0};
 }
 
+// ======================================================== candidate merge
+// The candidate rows' merge (top-k and/or top-p, sampling.py:75-90 and the
+// draw :94-98).  The row's candidate slots are spread so that every chunk
+// belongs to one wave: wave w holds chunks w, w + 8, ... (capc slots each),
+// lane l's slot j being wave-local slot L = 64 j + l, i.e. chunk
+// w + 8 (L / capc), chunk slot L % capc.  Per-chunk sums are then wave
+// reductions, and the draw inside the chunk that holds the inverse-CDF
+// point is finished by that chunk's wave alone.
+constexpr int kMS = kCandCap / kThreads;  // candidate slots per lane
+
+struct MCands {
+  double z[kMS];    // penalised logit
+  uint64_t w[kMS];  // fixed-point probability while kept, else 0
+  int idx[kMS];     // token id
+  uint32_t valid;   // bit j: slot j holds a candidate
+};
+
+// Chunk group of slot j (uniform: capc is a power of two >= 64) and its
+// chunk slot.
+__device__ __forceinline__ int mc_group(int j, int capc) { return (kWave * j) / capc; }
+__device__ __forceinline__ int mc_slot(int j, int capc) { return (kWave * j + lane()) & (capc - 1); }
+
+// Loads the slots j whose chunk slot lies in [s0, s1) and below the
+// chunk's candidate count (wc, this wave's copy); marks them valid.
+__device__ __forceinline__ void mc_load(const SampleArgs& a, int row, MCands& mc, const int* wc, int s0, int s1) {
+  const int C = a.ws.C, capc = a.ws.capc;
+  const size_t base = (size_t)row * C * capc;
+#pragma unroll
+  for (int j = 0; j < kMS; ++j) {
+    const int c = wave() + kWaves * mc_group(j, capc);
+    const int s = mc_slot(j, capc);
+    if (c < C && s >= s0 && s < s1 && s < wc[c]) {
+      const size_t i = base + (size_t)c * capc + s;
+      mc.z[j] = a.ws.cz[i];
+      mc.idx[j] = a.ws.ci[i];
+      mc.valid |= 1u << j;
+    }
+  }
+}
+
+// The slots below chunk slot smax, loaded before the counts are known
+// (top-p rows: every slot, their chunks fill nearly all of them; top-k rows:
+// the first 128 of each chunk); validity is set once the counts are in.
+__device__ __forceinline__ void mc_load_first(const SampleArgs& a, int row, MCands& mc, int smax) {
+  const int C = a.ws.C, capc = a.ws.capc;
+  const size_t base = (size_t)row * C * capc;
+#pragma unroll
+  for (int j = 0; j < kMS; ++j) {
+    const int c = wave() + kWaves * mc_group(j, capc);
+    mc.z[j] = -INFINITY;
+    mc.idx[j] = 0;
+    mc.w[j] = 0ull;
+    if (c < C && mc_slot(j, capc) < smax) {
+      const size_t i = base + (size_t)c * capc + mc_slot(j, capc);
+      mc.z[j] = a.ws.cz[i];
+      mc.idx[j] = a.ws.ci[i];
+    }
+  }
+}
+
+// Marks the loaded slots that hold candidates, then loads the rest of a
+// chunk whose candidates run past smax.
+__device__ __forceinline__ void mc_validate(const SampleArgs& a, int row, MCands& mc, const int* wc, int smax) {
+  const int C = a.ws.C, capc = a.ws.capc;
+  mc.valid = 0;
+  bool more = false;
+#pragma unroll
+  for (int j = 0; j < kMS; ++j) {
+    const int c = wave() + kWaves * mc_group(j, capc);
+    const int s = mc_slot(j, capc);
+    if (c < C && s < wc[c] && s < smax) mc.valid |= 1u << j;
+    more |= c < C && s >= smax && s < wc[c];
+  }
+  if (__ballot(more) != 0ull) mc_load(a, row, mc, wc, smax, capc);
+}
+
+struct ZSel {
+  bool found;
+  bool giveup;
+  double z;
+  int idx;
+};
+
+// Workgroup min and max of the active values (one cross-wave combine).
+__device__ __forceinline__ void active_range(uint32_t act, const MCands& mc, bool by_idx, int V, XWave& xw, double* lo,
+                                             double* hi) {
+  double a = INFINITY, b = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kMS; ++j)
+    if ((act >> j) & 1u) {
+      const double v = by_idx ? (double)(V - 1 - mc.idx[j]) : mc.z[j];
+      a = fmin(a, v);
+      b = fmax(b, v);
+    }
+  const auto s = xw.post(bits_of(wave_min(a)), bits_of(wave_max(b)), 0);
+  a = dbl_of(s[0][0]);
+  b = dbl_of(s[1][0]);
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    a = fmin(a, dbl_of(s[0][w]));
+    b = fmax(b, dbl_of(s[1][w]));
+  }
+  *lo = uniform(a);
+  *hi = uniform(b);
+}
+
+// Selection over the active slots in (z descending, token index ascending)
+// order, sampling.py:76-77 and :83-86:
+//   MASS=false: the target-th entry (its z: the top-k threshold);
+//   MASS=true : the first entry whose inclusive weight reaches target (the
+//               top-p cut).
+// Levels of kHB affine value bins over [lo, hi] (every active z lies there,
+// n bounds their count from above) keep the bin where the running count or
+// weight crosses the target, until one wave's worth is left; the rank list
+// then orders those exactly.  A level that separates nothing narrows the
+// range to the values' own; equal values are ordered by token index (levels
+// over V - 1 - index).
+template <bool MASS>
+__device__ __forceinline__ ZSel select_z(uint32_t act, const MCands& mc, double lo, double hi, uint32_t n,
+                                         uint64_t target, int V, RankList& rl, FastSmem& fs, XWave& xw, int& hgen) {
+  // the barrier the first level or the rank list relies on: the kernel
+  // zeroes the first histogram and the rank lists at its start
+  wg_barrier();
+  if (n == 0 || (!MASS && n < target)) return ZSel{false, false, 0.0, 0};
+  target = uniform(target);
+  uint32_t cnt = n;
+  uint64_t above = 0;
+  bool by_idx = false;
+  double vlo = lo, vhi = hi;
+  auto val = [&](int j) -> double { return by_idx ? (double)(V - 1 - mc.idx[j]) : mc.z[j]; };
+  for (int lev = 0; cnt > (uint32_t)kWave; ++lev) {
+    if (lev == kMaxLevels) return ZSel{false, true, 0.0, 0};
+    if (!(vhi > vlo)) {
+      // every active value is vlo
+      if (!MASS) return ZSel{true, false, vlo, 0};
+      if (by_idx) return ZSel{false, true, 0.0, 0};
+      by_idx = true;
+      vlo = 0.0;
+      vhi = (double)(V - 1);
+    }
+    const Affine af = make_affine(vlo, vhi, kHB);
+    Hist& h = next_hist(fs, hgen);
+#pragma unroll
+    for (int j = 0; j < kMS; ++j)
+      if ((act >> j) & 1u) {
+        const int b = af.bin(val(j));
+        lds_add(&h.cnt[b], 1u);
+        if (MASS) lds_add(&h.mass[b], mc.w[j]);
+      }
+    wg_barrier();
+    const WPick pk = wave_pick_desc<MASS>(h, above, target);
+    if (!pk.found) return ZSel{false, false, 0.0, 0};
+    above = uniform(pk.above);
+    const int d = uniform(pk.d);
+    const uint32_t ncnt = (uint32_t)uniform((int)h.cnt[d]);
+#pragma unroll
+    for (int j = 0; j < kMS; ++j)
+      if (((act >> j) & 1u) && af.bin(val(j)) != d) act &= ~(1u << j);
+    if (ncnt == cnt) {
+      active_range(act, mc, by_idx, V, xw, &vlo, &vhi);  // nothing separated: the values' own range
+    } else {
+      const double w = 1.0 / af.scale;
+      vlo = af.lo + (double)d * w;
+      vhi = d == kHB - 1 ? vhi : af.lo + (double)(d + 1) * w;
+    }
+    cnt = ncnt;
+  }
+  // rank list: one LDS reservation per wave
+  const int nq = __popc(act);
+  const int qi = wave_scan_incl(nq, 0, OpAdd{});
+  int rbase = 0;
+  if (lane() == kWave - 1 && qi > 0) rbase = lds_fetch_add(&rl.n, qi);
+  int slot = lane_value(rbase, kWave - 1) + qi - nq;
+#pragma unroll
+  for (int j = 0; j < kMS; ++j)
+    if ((act >> j) & 1u) {
+      rl.key[slot] = key_of(mc.z[j]);
+      rl.idx[slot] = mc.idx[j];
+      rl.w[slot] = MASS ? mc.w[j] : 0ull;
+      ++slot;
+    }
+  wg_barrier();
+  // lane i of every wave holds entry i; wave w compares it with entries
+  // j in [8w, 8w + 8) (LDS broadcast reads) and adds its counts to the
+  // entry's totals
+  const int m = uniform(rl.n);
+  const int ln = lane();
+  uint64_t k = 0ull, wt = 0ull;
+  int ix = INT_MAX;
+  if (ln < m) {
+    k = rl.key[ln];
+    ix = rl.idx[ln];
+    wt = rl.w[ln];
+  }
+  uint32_t rank = 0;
+  uint64_t ahead = 0;
+  constexpr int kPerWave = kWave / kWaves;
+#pragma unroll
+  for (int jj = 0; jj < kPerWave; ++jj) {
+    const int j = wave() * kPerWave + jj;
+    if (j < m) {
+      const uint64_t kj = rl.key[j];
+      const int ij = rl.idx[j];
+      const bool bj = kj > k || (kj == k && ij < ix);
+      rank += bj ? 1u : 0u;
+      if (MASS) ahead += bj ? rl.w[j] : 0ull;
+    }
+  }
+  if (ln < m) {
+    lds_add(&rl.rank[ln], rank);
+    if (MASS) lds_add(&rl.ahead[ln], ahead);
+  }
+  wg_barrier();
+  if (ln < m) {
+    rank = rl.rank[ln];
+    ahead = rl.ahead[ln];
+  }
+  bool hit;
+  if (!MASS) hit = ln < m && (uint64_t)rank == target - above - 1;
+  else hit = ln < m && above + ahead < target && above + ahead + wt >= target;
+  const uint64_t hits = __ballot(hit);
+  if (hits == 0) return ZSel{false, !MASS, 0.0, 0};
+  const int L = __builtin_ctzll(hits);
+  return ZSel{true, false, val_of_key(lane_value(k, L)), lane_value(ix, L)};
+}
+
+// Inverse-CDF draw over the kept slots in vocabulary order (sampling.py:94-98):
+// the first token whose running fixed-point mass exceeds floor(u * total),
+// V - 1 when none does.  The chunk holding that point comes from the
+// per-chunk kept sums (each chunk's wave sums its own); that chunk's wave
+// then locates the token alone, through index bins of the chunk's tokens
+// and the crossing bin's tokens laid out by offset.  Returns the id in the
+// lanes of the chunk's wave and -1 in the other waves.
+template <typename TIn>
+__device__ __forceinline__ int draw_chunks(const SampleArgs& a, const MCands& mc, double u, FastSmem& fs) {
+  using G = Geo<TIn>;
+  const int C = a.ws.C, capc = a.ws.capc, V = a.V;
+  constexpr int kTokPerBin = G::kChunk / kHB;  // 16 (float) or 8 (double) tokens per index bin
+  static_assert(kTokPerBin <= kDrawSpanMax, "span");
+  // per-chunk kept sums: wave w posts chunks w, w + 8, ...
+  const int ng = (C + kWaves - 1) / kWaves;
+  for (int g = 0; g < ng; ++g) {
+    uint64_t s = 0;
+#pragma unroll
+    for (int j = 0; j < kMS; ++j)
+      if (mc_group(j, capc) == g) s += mc.w[j];
+    s = wave_sum(s);
+    const int c = wave() + kWaves * g;
+    if (lane() == 0 && c < C) fs.csum[c] = s;
+  }
+  wg_barrier();
+  // every wave: the total, and the chunk where the running mass crosses t
+  uint64_t cs = lane() < C ? fs.csum[lane()] : 0ull;  // C <= kWave
+  const uint64_t incl = wave_scan_incl(cs, (uint64_t)0, OpAdd{});
+  const uint64_t tot = lane_value(incl, kWave - 1);
+  if (tot == 0) return V - 1;
+  const uint64_t t = (uint64_t)__double2ull_rd(u * (double)tot);
+  const uint64_t hits = __ballot(incl - cs <= t && t < incl && lane() < C);
+  if (hits == 0) return V - 1;
+  const int cstar = __builtin_ctzll(hits);
+  const uint64_t before = uniform(lane_value(incl - cs, cstar));
+  if (wave() != cstar % kWaves) return -1;
+  // the chunk's wave: index bins of kTokPerBin tokens over the chunk
+  const int gstar = cstar / kWaves;
+  const int c0 = cstar * G::kChunk;
+  uint64_t* hb = fs.h[0].mass;  // this wave alone uses it from here on
+  for (int b = lane(); b < kHB; b += kWave) hb[b] = 0ull;
+#pragma unroll
+  for (int j = 0; j < kMS; ++j)
+    if (mc_group(j, capc) == gstar && mc.w[j] != 0ull) lds_add(&hb[(mc.idx[j] - c0) / kTokPerBin], mc.w[j]);
+  // lane l sums bins [16l, 16l + 16) (rotated reads spread the banks)
+  constexpr int kPer = kHB / kWave;
+  const int b0 = kPer * lane();
+  uint64_t s = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) s += hb[b0 + ((j + lane()) & (kPer - 1))];
+  const uint64_t in2 = wave_scan_incl(s, (uint64_t)0, OpAdd{});
+  const uint64_t ex2 = before + in2 - s;
+  const uint64_t h2 = __ballot(ex2 <= t && t < before + in2);
+  if (h2 == 0) return V - 1;
+  const int L = __builtin_ctzll(h2);
+  int bl = 0;
+  uint64_t bf = 0;
+  if (lane() == L) {
+    uint64_t run = ex2;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const uint64_t v = hb[b0 + j];
+      if (run <= t && t < run + v) {
+        bl = b0 + j;
+        bf = run;
+      }
+      run += v;
+    }
+  }
+  const int b = uniform(lane_value(bl, L));
+  const uint64_t bbefore = uniform(lane_value(bf, L));
+  // the bin's kept tokens by offset
+  if (lane() < kTokPerBin) fs.dspan[lane()] = 0ull;
+#pragma unroll
+  for (int j = 0; j < kMS; ++j)
+    if (mc_group(j, capc) == gstar && mc.w[j] != 0ull && (mc.idx[j] - c0) / kTokPerBin == b)
+      fs.dspan[mc.idx[j] - c0 - b * kTokPerBin] = mc.w[j];
+  const uint64_t v = lane() < kTokPerBin ? fs.dspan[lane()] : 0ull;
+  const uint64_t in3 = wave_scan_incl(v, (uint64_t)0, OpAdd{});
+  const uint64_t h3 = __ballot(v != 0ull && bbefore + in3 - v <= t && t < bbefore + in3);
+  if (h3 == 0) return V - 1;
+  return c0 + b * kTokPerBin + __builtin_ctzll(h3);
+}
+
+// Top-k and/or top-p rows from the chunk candidates (sampling.py:75-90,
+// :94-98).  id: the drawn token in the lanes of the wave that drew it, -1 in
+// the others.
+struct CandOut {
+  int id;
+  bool general;  // the candidates cannot decide the row exactly (uniform)
+  double S;      // general: the full normaliser when known (top-p-only rows), else 0
+};
+
+template <typename TIn, bool TOPK>
+__device__ __forceinline__ CandOut merge_cands(const SampleArgs& a, MCands& mc, const SegLoad& sg, const RowParams& rp,
+                                               const PartSum& ps, FastSmem& fs, XWave& xw, int& hgen) {
+  const int V = a.V;
+  const double* tab = fs.exp_tab[wave()];
+  const int* wc = fs.wcnt[wave()];
+  auto count_cands = [&]() -> uint32_t {
+    int nc = 0;
+    for (int c = lane(); c < a.ws.C; c += kWave) nc += wc[c];
+    return (uint32_t)uniform(wave_sum(nc));
+  };
+  const double T = rp.T;
+  auto yexact = [&](double z) -> double { return T == 1.0 ? z : z / T; };
+
+  // ---- top-k: k-th largest with multiplicity, keep y >= kth_y (:76-78)
+  double z_lo = -INFINITY;
+  uint32_t act = mc.valid;
+  if (TOPK) {
+    // every candidate lies in [the smallest chunk threshold, the row max]
+    const double lo = ps.umin > -INFINITY ? ps.umin : -1.7976931348623157e308;
+    const ZSel r = select_z<false>(act, mc, lo, ps.zmax, count_cands(), (uint64_t)rp.top_k, V, fs.rl[0], fs, xw, hgen);
+    if (!r.found) return CandOut{V - 1, true, 0.0};
+    const double kth_y = yexact(r.z);
+    z_lo = r.z;
+    for (int it = 0; it < 64; ++it) {
+      const double zp = dbl_prev(z_lo);
+      if (yexact(zp) >= kth_y) z_lo = zp;
+      else break;
+    }
+    if (!(ps.umax < z_lo)) return CandOut{V - 1, true, 0.0};
+  }
+
+  // ---- softmax (:79-81): p = exp(y - ymax) / S, once per kept candidate
+  const YScale ys{T, 1.0 / T};
+  const double ymax = ys(ps.zmax);
+  double s = 0.0;
+  uint32_t nkept = 0;
+#pragma unroll
+  for (int j = 0; j < kMS; ++j) {
+    const bool k = ((act >> j) & 1u) && mc.z[j] >= z_lo;
+    const double e = k ? fast_exp_neg(ys(mc.z[j]) - ymax, tab) : 0.0;
+    mc.w[j] = bits_of(e);  // the weight slot holds e until S is known
+    nkept += k ? 1u : 0u;
+    s += e;
+  }
+  double S;
+  uint32_t nk;
+  if (TOPK) {
+    const auto sk = xw.post(bits_of(wave_sum(s)), (uint64_t)wave_sum(nkept), 0);
+    S = 0.0;
+    nk = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      S += dbl_of(sk[0][w]);
+      nk += (uint32_t)sk[1][w];
+    }
+  } else {
+    double ms[kSegPerLane], lex;
+    S = seg_norm(sg, tab, ms, &lex).S;
+    nk = count_cands();
+  }
+  const double invS = 1.0 / S;
+  uint32_t pos = 0;
+#pragma unroll
+  for (int j = 0; j < kMS; ++j) {
+    const double p = dbl_of(mc.w[j]) * invS;
+    mc.w[j] = to_fx(p);
+    if (p > 0.0) pos |= 1u << j;
+  }
+
+  // ---- top-p: first token (p desc, index asc) whose inclusive mass reaches
+  // top_p (:82-90), in (z desc, index asc) order
+  if (rp.topp) {
+    const double lo = TOPK ? z_lo : (ps.umin > -INFINITY ? ps.umin : -1.7976931348623157e308);
+    const ZSel r = select_z<true>(pos, mc, lo, ps.zmax, nk, topp_target(rp.top_p), V, fs.rl[1], fs, xw, hgen);
+    if (r.giveup) return CandOut{V - 1, true, TOPK ? 0.0 : S};
+    if (r.found) {
+#pragma unroll
+      for (int j = 0; j < kMS; ++j)
+        if (!(mc.z[j] > r.z || (mc.z[j] == r.z && mc.idx[j] <= r.idx))) mc.w[j] = 0ull;
+    }
+    if (!TOPK && ps.umax > -INFINITY) {
+      // the largest token left out must fall outside the nucleus
+      const double pU = fast_exp_neg(ys(ps.umax) - ymax, tab) * invS;
+      const double pC = r.found ? fast_exp_neg(ys(r.z) - ymax, tab) * invS : 0.0;
+      if (!(r.found && pC > pU)) return CandOut{V - 1, true, S};
+    }
+  }
+
+  // ---- draw in vocabulary order (:94-98)
+  return CandOut{draw_chunks<TIn>(a, mc, rp.u, fs), false, 0.0};
+}
+
 template <typename TIn, bool VEC, bool NUC>
 __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   __shared__ SmemAll sm;
@@ -1518,18 +1944,19 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   }
   XWave xw{fs.xw, 0};
   int hgen = 0;
-  // global loads first: candidates (top-p rows, whose chunks fill nearly
-  // every slot), segment partials, then the wave parts; top-k rows then
-  // read only the slots their chunks filled (typically a few percent)
-  RegCands rc;
-  const bool gather_early = cands && !rp.topk;
-  if (gather_early) gather_cands(a, row, rc);
+  // global loads first: candidates (top-p rows: every slot, their chunks
+  // fill nearly all; top-k rows: the first 128 of each chunk), segment
+  // partials, then the wave parts; a top-k chunk with more candidates is
+  // read once the counts are in
+  MCands mc;
+  const int smax = rp.topk ? min(128, a.ws.capc) : a.ws.capc;
+  if (cands) mc_load_first(a, row, mc, smax);
   SegLoad sg;
   if (!rp.greedy && !rp.topk && !(NUC && rp.nucleus)) {  // nucleus rows only set their bin range here
     load_segs(a, row, (a.V + Geo<TIn>::kSeg - 1) / Geo<TIn>::kSeg, sg);
   }
   const PartSum ps = scan_parts(a, row, rp.greedy, cands, fs);
-  if (cands && !gather_early) gather_cands(a, row, rc, fs.wcnt[wave()]);
+  if (cands) mc_validate(a, row, mc, fs.wcnt[wave()], smax);
   // a chunk that could not keep all its penalised tokens aside sends the
   // row to the general pipeline
   bool general = ps.flags != 0;
@@ -1569,10 +1996,14 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   } else if (!cands) {
     id = finish_temp<TIn>(a, row, rp, sg, fs, xw);
   } else {
-    const FastOut o = rp.topk ? finish_cands<TIn, true>(a, rc, sg, rp, ps, fs, xw, hgen)
-                              : finish_cands<TIn, false>(a, rc, sg, rp, ps, fs, xw, hgen);
-    id = o.id;
+    const CandOut o = rp.topk ? merge_cands<TIn, true>(a, mc, sg, rp, ps, fs, xw, hgen)
+                              : merge_cands<TIn, false>(a, mc, sg, rp, ps, fs, xw, hgen);
     general = o.general;
+    if (!general) {
+      // the id is known in the lanes of the wave that drew it
+      if (lane() == 0 && o.id >= 0) a.out_ids[row] = o.id;
+      return;
+    }
     pin = PipeIn{true, ps.zmax, o.S > 0.0, o.S, false, 0.0};
   }
   if (general) {
@@ -1653,7 +2084,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   __shared__ ChunkSmem cm;
   __shared__ uint32_t nh[kNucBins];
   const int C = a.ws.C;
-  const int g = blockIdx.x;
+  const int g = chunk_block(C, a.B);
+  if (g < 0) return;
   const int row = g / C;
   const RowParams rp = load_row_params(a, row);
   if (!rp.nucleus) return;
@@ -1830,7 +2262,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   __shared__ int over;
   const int C = a.ws.C;
   const int capc = a.ws.capc;
-  const int g = blockIdx.x;
+  const int g = chunk_block(C, a.B);
+  if (g < 0) return;
   const int row = g / C;
   const RowParams rp = load_row_params(a, row);
   if (!rp.nucleus) return;
@@ -2234,7 +2667,7 @@ hipError_t launch_sample_rows(const SampleArgs& a, bool f64, bool vec, hipStream
 
 hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, int num_cu, hipStream_t s, hipEvent_t between) {
   (void)num_cu;
-  const int total = a.B * a.ws.C;
+  const int total = kXcds * ((a.B + kXcds - 1) / kXcds) * a.ws.C;  // blocks of the chunk grids (chunk_block)
   const dim3 gf(a.B), block(kThreads);
   // the nucleus code is compiled only into the instantiations the hint selects
   using K = void (*)(SampleArgs);
