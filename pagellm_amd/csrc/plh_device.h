@@ -195,6 +195,10 @@ struct OpMax {
   template <typename T>
   __device__ __forceinline__ T operator()(T a, T b) const { return b > a ? b : a; }
 };
+struct OpOr {
+  template <typename T>
+  __device__ __forceinline__ T operator()(T a, T b) const { return a | b; }
+};
 struct OpMin {
   template <typename T>
   __device__ __forceinline__ T operator()(T a, T b) const { return b < a ? b : a; }

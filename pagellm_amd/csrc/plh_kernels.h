@@ -39,6 +39,8 @@ struct NucRow {
 constexpr int kNucActive = 1;
 constexpr int kNucPenWords = 512;  // bitmap words of one chunk (16384 float tokens)
 constexpr int kNucBins = 2048;
+constexpr int kBkt = 256;          // candidate buckets of a top-p chunk
+constexpr double kBktPerY = 8.0;   // buckets per unit of y (the last bucket is open below)
 
 // Workspace of the two-launch fast path, carved from one device buffer.
 struct ChunkWs {
@@ -52,6 +54,13 @@ struct ChunkWs {
   double* nexcl;    // [B * C * 8] nucleus path: per-segment mass on one side of the candidate bins
   int32_t* ncand;   // [B * C] nucleus path: candidates per chunk (-1: over capacity)
   uint32_t* npen;   // [B * C * kNucPenWords] nucleus path: each chunk's penalised-token bitmap
+  // top-p rows (no top-k): each chunk's candidates in buckets of an absolute
+  // grid of y = z / T (kBktPerY buckets per unit, bucket 0 the chunk's top),
+  // written bucket by bucket, each with exp(y - the chunk's max y)
+  uint64_t* bmass;  // [B * C * kBkt] per bucket: sum of exp(y - ymax_c) * 2^52
+  uint32_t* bcnt;   // [B * C * kBkt] per bucket: candidates
+  double* bymax;    // [B * C] the chunk's max y
+  int32_t* bhb;     // [B * C] the chunk's top bucket: floor(ymax_c * kBktPerY)
   int C;            // chunks per row
   int capc;         // candidate slots per chunk
 };

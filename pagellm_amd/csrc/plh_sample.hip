@@ -86,6 +86,8 @@ struct FastSmem {
   Hist h[kHBuf];
   uint64_t dspan[kDrawSpanMax];       // the draw's crossing bin, by token offset
   uint64_t csum[kMaxChunks];          // the draw's per-chunk kept mass
+  uint64_t rowm[kBkt];                // top-p rows: the row's bucket masses
+  int cq0[kMaxChunks], cq1[kMaxChunks];  // top-p rows: each chunk's list range of the cut bucket
   RankList rl[2];                     // top-k, top-p
   uint32_t segbits[kSegMax / 32];     // penalty bits of a rescanned segment
 };
@@ -159,7 +161,7 @@ struct VecOf<double> {
 // with more makes its chunk incomplete (the row takes the general
 // pipeline).
 constexpr int kPenPerWave = 128;
-constexpr uint32_t kCodePen = 0xffffffffu;  // a staged slot written directly (penalised token)
+constexpr uint32_t kCodePool = 0x80000000u;  // a staged penalised token: | wave << 8 | its entry in the wave's pool
 
 // Raw input values of staged candidates (float32 or float64 bits).
 union StageRaw {
@@ -182,7 +184,7 @@ struct ChunkSmem {
   double pz[kWaves][kPenPerWave];
   int pt[kWaves][kPenPerWave];
   // candidates staged on their way to the workspace: the raw value and
-  // its token index (kCodePen for a penalised token written directly);
+  // its token index (kCodePool | wave | pool entry for a penalised token);
   // float inputs keep both in one 8-byte pair, (float bits, index)
   union {
     StageRaw sraw[kCapChunk];
@@ -190,6 +192,11 @@ struct ChunkSmem {
   };
   uint32_t scode[kCapChunk];
   int cand_n;
+  // top-p rows: candidate buckets (kBkt of them, bucket 0 the chunk's top)
+  uint32_t bcnt[kBkt];
+  uint64_t bmass[kBkt];
+  int boff[kBkt];
+  int bcur[kBkt];
 };
 
 // Chunk-local offset of the calling lane's register slot e: the lane's
@@ -479,6 +486,116 @@ __device__ __forceinline__ int hist_reach_desc(const uint32_t* h, uint32_t targe
   return base - __builtin_ctzll(hit);
 }
 
+// A staged candidate: its penalised logit and token id (penalised tokens
+// from their entry in the wave's pool).
+template <typename TIn>
+__device__ __forceinline__ void staged(const ChunkSmem& cm, int i, double* z, int* id) {
+  uint32_t code;
+  double x;
+  if constexpr (sizeof(TIn) == 4) {
+    const uint2 pr = cm.spair[i];
+    code = pr.y;
+    x = (double)__uint_as_float(pr.x);
+  } else {
+    code = cm.scode[i];
+    x = cm.sraw[i].d;
+  }
+  if (code & kCodePool) {
+    const int w = (int)((code >> 8) & 0x7fu), e = (int)(code & 0xffu);
+    *z = cm.pz[w][e];
+    *id = cm.pt[w][e];
+  } else {
+    *z = x;
+    *id = (int)code;
+  }
+}
+
+// Top-p rows: the chunk's candidates go to the workspace bucket by bucket
+// (buckets of kBktPerY per unit of y = z * (1 / T) on an absolute grid,
+// bucket 0 the one holding the chunk's max y, the last one open below), each
+// as exp(y - ymax_c) and its token id, with the buckets' counts and masses
+// (exp sums in 2^-52 units; at most 1024 candidates keep them below 2^62).
+// The merge sums the buckets of a row's chunks, which line up on the
+// absolute grid, to find the one holding the top-p cut, and then reads only
+// that bucket's candidates, and the candidates of the chunk that holds the
+// draw.  Skipped when the chunk's candidates overflowed (the row then takes
+// the general pipeline).
+template <typename TIn>
+__device__ __forceinline__ void write_buckets(const SampleArgs& a, int g, double hi, double invT, ChunkSmem& cm) {
+  wg_barrier();  // every wave's candidates are staged
+  const int n = cm.cand_n;
+  const int capc = a.ws.capc;
+  if (n > capc) return;  // uniform; the chunk is incomplete and the row takes the general pipeline
+  if (!(hi > -INFINITY)) {  // no finite token: no candidates, an empty bucket set
+    if (threadIdx.x < kBkt) {
+      a.ws.bmass[(size_t)g * kBkt + threadIdx.x] = 0ull;
+      a.ws.bcnt[(size_t)g * kBkt + threadIdx.x] = 0u;
+    }
+    if (threadIdx.x == 0) {
+      a.ws.bymax[g] = -INFINITY;
+      a.ws.bhb[g] = INT_MIN;
+    }
+    return;
+  }
+  const double ymaxc = hi * invT;
+  const double hbc = __builtin_floor(ymaxc * kBktPerY);
+  const double* tab = cm.exp_tab[wave()];
+  constexpr int kPer = kCapChunk / kThreads;
+  double ev[kPer];
+  int idv[kPer], lbv[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int i = (int)threadIdx.x + k * kThreads;
+    lbv[k] = -1;
+    if (i < n) {
+      double z;
+      staged<TIn>(cm, i, &z, &idv[k]);
+      const double y = z * invT;
+      ev[k] = fast_exp_neg(y - ymaxc, tab);
+      const double d = hbc - __builtin_floor(y * kBktPerY);
+      const int lb = d < (double)(kBkt - 1) ? (int)d : kBkt - 1;
+      lbv[k] = lb;
+      lds_add(&cm.bcnt[lb], 1u);
+      lds_add(&cm.bmass[lb], (uint64_t)__double2ull_rn(ev[k] * 4503599627370496.0));
+    }
+  }
+  wg_barrier();
+  if (wave() == 0) {  // the buckets' offsets: exclusive prefix of the counts
+    constexpr int kB4 = kBkt / kWave;
+    uint32_t c[kB4], t = 0;
+#pragma unroll
+    for (int j = 0; j < kB4; ++j) {
+      c[j] = cm.bcnt[kB4 * lane() + j];
+      t += c[j];
+    }
+    uint32_t o = wave_scan_incl(t, 0u, OpAdd{}) - t;
+#pragma unroll
+    for (int j = 0; j < kB4; ++j) {
+      cm.boff[kB4 * lane() + j] = (int)o;
+      o += c[j];
+    }
+  }
+  if (threadIdx.x < kBkt) {
+    a.ws.bmass[(size_t)g * kBkt + threadIdx.x] = cm.bmass[threadIdx.x];
+    a.ws.bcnt[(size_t)g * kBkt + threadIdx.x] = cm.bcnt[threadIdx.x];
+  }
+  if (threadIdx.x == 0) {
+    a.ws.bymax[g] = ymaxc;
+    a.ws.bhb[g] = (int)hbc;
+  }
+  wg_barrier();
+  double* cz = a.ws.cz + (size_t)g * capc;
+  int32_t* ci = a.ws.ci + (size_t)g * capc;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    if (lbv[k] >= 0) {
+      const int pos = cm.boff[lbv[k]] + lds_fetch_add(&cm.bcur[lbv[k]], 1);
+      cz[pos] = ev[k];
+      ci[pos] = idv[k];
+    }
+  }
+}
+
 // Candidates of one chunk: every finite z >= theta, with theta below the
 // chunk's target-th largest token (all finite tokens when there are fewer).
 //   top-k, k <= 512: the k-th largest of the workgroup's 512 per-thread
@@ -505,8 +622,9 @@ __device__ __forceinline__ int hist_reach_desc(const uint32_t* h, uint32_t targe
 //   fl: every token of the wave is a float (no float64 pool entries).
 template <typename TIn>
 __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax, double wmax, TIn m2, bool by_max,
-                                                 uint64_t target, bool fl, const SampleArgs& a, int g, int c0,
-                                                 int flags, WavePart* wp, ChunkSmem& cm) {
+                                                 uint64_t target, bool fl, bool bucket, double invT,
+                                                 const SampleArgs& a, int g, int c0, int flags, WavePart* wp,
+                                                 ChunkSmem& cm) {
   using G = Geo<TIn>;
   constexpr int kEpt = G::kEpt;
   const int capc = a.ws.capc;
@@ -623,10 +741,7 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
     wend = base;
   } else {
     // register tokens: the raw value and the token index go to LDS; the
-    // penalised ones (few) straight to the workspace with their float64
-    // value and token id
-    double* cz = a.ws.cz + (size_t)g * capc;
-    int32_t* ci = a.ws.ci + (size_t)g * capc;
+    // penalised ones (few) a reference to their entry in the wave's pool
     const int idx0 = c0 + slot_q<TIn>(0);
     int pos = base;
     tk.new_pass();
@@ -653,29 +768,25 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
       const uint64_t m = __ballot(keep);
       if (keep) {
         const int s = pos + mbcnt(m, 0);
-        if constexpr (sizeof(TIn) == 4) cm.spair[s].y = kCodePen;
-        else cm.scode[s] = kCodePen;
-        cz[s] = z;
-        ci[s] = tk.pen_tok(cm, i);
+        const uint32_t code = kCodePool | ((uint32_t)wave() << 8) | (uint32_t)(lane() + kWave * i);
+        if constexpr (sizeof(TIn) == 4) cm.spair[s].y = code;
+        else cm.scode[s] = code;
       }
       pos += (int)__popcll(m);
     }
-    for (int i = base + lane(); i < wend; i += kWave) {
-      if constexpr (sizeof(TIn) == 4) {
-        const uint2 pr = cm.spair[i];
-        if (pr.y != kCodePen) {
-          cz[i] = (double)__uint_as_float(pr.x);
-          ci[i] = (int32_t)pr.y;
-        }
-      } else {
-        const uint32_t code = cm.scode[i];
-        if (code != kCodePen) {
-          cz[i] = cm.sraw[i].d;
-          ci[i] = (int32_t)code;
-        }
+    if (!bucket) {
+      double* cz = a.ws.cz + (size_t)g * capc;
+      int32_t* ci = a.ws.ci + (size_t)g * capc;
+      for (int i = base + lane(); i < wend; i += kWave) {
+        double z;
+        int id;
+        staged<TIn>(cm, i, &z, &id);
+        cz[i] = z;
+        ci[i] = id;
       }
     }
   }
+  if (bucket) write_buckets<TIn>(a, g, hi, invT, cm);
   // every token left out is below theta
   if (lane() == 0) {
     wp->zmax = hi;
@@ -720,6 +831,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   if (cands) {  // ordered before use by the first barrier of chunk_candidates
     for (int b = threadIdx.x; b < kHB; b += kThreads) cm.hcnt[b] = 0u;
     if (threadIdx.x == 0) cm.cand_n = 0;
+    if (!rp.topk && threadIdx.x < kBkt) {
+      cm.bcnt[threadIdx.x] = 0u;
+      cm.bmass[threadIdx.x] = 0ull;
+      cm.bcur[threadIdx.x] = 0;
+    }
   }
   int flags = 0;
   if (rp.pen_active) {
@@ -776,7 +892,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   // tokens are all in the registers, in the input precision
   const bool fl = sizeof(TIn) == 4 && uniform(tk.np) == 0;
   const double wmax = uniform(wave_max_fd(lmax, fl));
-  if (cands) chunk_candidates<TIn>(tk, lmax, wmax, m2, by_max, target, fl, a, g, c0, flags, wp, cm);
+  if (cands) chunk_candidates<TIn>(tk, lmax, wmax, m2, by_max, target, fl, !rp.topk && C <= kWaves, 1.0 / rp.T, a, g, c0,
+                                     flags, wp, cm);
   else if (lane() == 0) wp->flags = flags;
   if (NUC && rp.nucleus && g == row * C)  // the row's count histogram, filled by k_nuc_hist
     for (int b = threadIdx.x; b < kNucBins; b += kThreads) a.ws.ncnt[(size_t)row * kNucBins + b] = 0u;
@@ -1525,7 +1642,14 @@ struct MCands {
   uint64_t w[kMS];  // fixed-point probability while kept, else 0
   int idx[kMS];     // token id
   uint32_t valid;   // bit j: slot j holds a candidate
+  uint32_t jm;      // bit j: slot j holds a candidate in some lane of the wave (uniform)
 };
+
+// Loops over a lane's slots skip, with a uniform branch, the slots that
+// hold no candidate anywhere in the wave (a top-k row's chunk fills one or
+// two of its wave's 16).
+#define MC_FOR(j, mc) \
+  _Pragma("unroll") for (int j = 0; j < kMS; ++j) if (((mc).jm >> j) & 1u)
 
 // Chunk group of slot j (uniform: capc is a power of two >= 64) and its
 // chunk slot.
@@ -1570,6 +1694,22 @@ __device__ __forceinline__ void mc_load_first(const SampleArgs& a, int row, MCan
   }
 }
 
+// The slots with chunk slot in [s0, s1), loaded before the counts are known.
+__device__ __forceinline__ void mc_load_range(const SampleArgs& a, int row, MCands& mc, int s0, int s1) {
+  const int C = a.ws.C, capc = a.ws.capc;
+  const size_t base = (size_t)row * C * capc;
+#pragma unroll
+  for (int j = 0; j < kMS; ++j) {
+    const int c = wave() + kWaves * mc_group(j, capc);
+    const int s = mc_slot(j, capc);
+    if (c < C && s >= s0 && s < s1) {
+      const size_t i = base + (size_t)c * capc + s;
+      mc.z[j] = a.ws.cz[i];
+      mc.idx[j] = a.ws.ci[i];
+    }
+  }
+}
+
 // Marks the loaded slots that hold candidates, then loads the rest of a
 // chunk whose candidates run past smax.
 __device__ __forceinline__ void mc_validate(const SampleArgs& a, int row, MCands& mc, const int* wc, int smax) {
@@ -1584,6 +1724,7 @@ __device__ __forceinline__ void mc_validate(const SampleArgs& a, int row, MCands
     more |= c < C && s >= smax && s < wc[c];
   }
   if (__ballot(more) != 0ull) mc_load(a, row, mc, wc, smax, capc);
+  mc.jm = (uint32_t)__builtin_amdgcn_readlane((int)wave_scan_incl(mc.valid, 0u, OpOr{}), kWave - 1);
 }
 
 struct ZSel {
@@ -1593,17 +1734,64 @@ struct ZSel {
   int idx;
 };
 
+// Every wave on its own: the bin of h where the running total (bins taken
+// from the highest down, starting at `above`) first reaches target.  Lane l
+// sums the 16 bins of group 63 - l with 16-byte LDS reads and a wave scan
+// finds the group; the 16 lanes of each row then read one bin of that group
+// each, highest first, and a row scan finds the bin.  The running total is
+// non-decreasing, so exactly one bin takes it from below target to target
+// or more.
+template <bool MASS>
+__device__ __forceinline__ WPick wave_pick2(const Hist& h, uint64_t above, uint64_t target) {
+  constexpr int PL = kHB / kWave;
+  static_assert(PL == 16, "one 16-lane row per group");
+  const int grp = kWave - 1 - lane();
+  uint64_t s = 0;
+  if (MASS) {
+    const uint4* hv = reinterpret_cast<const uint4*>(h.mass + grp * PL);
+#pragma unroll
+    for (int i = 0; i < PL / 2; ++i) {
+      const uint4 q = hv[i];
+      s += (((uint64_t)q.y << 32) | q.x) + (((uint64_t)q.w << 32) | q.z);
+    }
+  } else {
+    const uint4* hv = reinterpret_cast<const uint4*>(h.cnt + grp * PL);
+#pragma unroll
+    for (int i = 0; i < PL / 4; ++i) {
+      const uint4 q = hv[i];
+      s += (uint64_t)((q.x + q.y) + (q.z + q.w));
+    }
+  }
+  const uint64_t incl = wave_scan_incl(s, (uint64_t)0, OpAdd{});
+  const uint64_t tot = lane_value(incl, kWave - 1);
+  if (above >= target || above + tot < target) return WPick{false, -1, above + tot};
+  const uint64_t cross = __ballot(above + incl - s < target && above + incl >= target);
+  const int lc = __builtin_ctzll(cross);
+  const uint64_t gab = above + lane_value(incl - s, lc);  // the total above the group
+  const int top = (kWave - 1 - lc) * PL + PL - 1;         // the group's highest bin
+  const int j = lane() & (PL - 1);
+  const uint64_t v = MASS ? h.mass[top - j] : (uint64_t)h.cnt[top - j];
+  uint64_t r = v;
+  r += dpp<kDppRowShr1, 0xf>((uint64_t)0, r);
+  r += dpp<kDppRowShr2, 0xf>((uint64_t)0, r);
+  r += dpp<kDppRowShr4, 0xf>((uint64_t)0, r);
+  r += dpp<kDppRowShr8, 0xf>((uint64_t)0, r);
+  const uint64_t hit = __ballot(gab + r >= target) & 0xffffull;
+  const int jj = __builtin_ctzll(hit);
+  return WPick{true, top - jj, gab + lane_value(r - v, jj)};
+}
+
 // Workgroup min and max of the active values (one cross-wave combine).
 __device__ __forceinline__ void active_range(uint32_t act, const MCands& mc, bool by_idx, int V, XWave& xw, double* lo,
                                              double* hi) {
   double a = INFINITY, b = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < kMS; ++j)
+  MC_FOR(j, mc) {
     if ((act >> j) & 1u) {
       const double v = by_idx ? (double)(V - 1 - mc.idx[j]) : mc.z[j];
       a = fmin(a, v);
       b = fmax(b, v);
     }
+  }
   const auto s = xw.post(bits_of(wave_min(a)), bits_of(wave_max(b)), 0);
   a = dbl_of(s[0][0]);
   b = dbl_of(s[1][0]);
@@ -1629,14 +1817,15 @@ __device__ __forceinline__ void active_range(uint32_t act, const MCands& mc, boo
 // over V - 1 - index).
 template <bool MASS>
 __device__ __forceinline__ ZSel select_z(uint32_t act, const MCands& mc, double lo, double hi, uint32_t n,
-                                         uint64_t target, int V, RankList& rl, FastSmem& fs, XWave& xw, int& hgen) {
+                                         uint64_t target, int V, RankList& rl, FastSmem& fs, XWave& xw, int& hgen,
+                                         uint64_t above0 = 0) {
   // the barrier the first level or the rank list relies on: the kernel
   // zeroes the first histogram and the rank lists at its start
   wg_barrier();
   if (n == 0 || (!MASS && n < target)) return ZSel{false, false, 0.0, 0};
   target = uniform(target);
   uint32_t cnt = n;
-  uint64_t above = 0;
+  uint64_t above = uniform(above0);
   bool by_idx = false;
   double vlo = lo, vhi = hi;
   auto val = [&](int j) -> double { return by_idx ? (double)(V - 1 - mc.idx[j]) : mc.z[j]; };
@@ -1652,22 +1841,22 @@ __device__ __forceinline__ ZSel select_z(uint32_t act, const MCands& mc, double 
     }
     const Affine af = make_affine(vlo, vhi, kHB);
     Hist& h = next_hist(fs, hgen);
-#pragma unroll
-    for (int j = 0; j < kMS; ++j)
+    MC_FOR(j, mc) {
       if ((act >> j) & 1u) {
         const int b = af.bin(val(j));
         lds_add(&h.cnt[b], 1u);
         if (MASS) lds_add(&h.mass[b], mc.w[j]);
       }
+    }
     wg_barrier();
-    const WPick pk = wave_pick_desc<MASS>(h, above, target);
+    const WPick pk = wave_pick2<MASS>(h, above, target);
     if (!pk.found) return ZSel{false, false, 0.0, 0};
     above = uniform(pk.above);
     const int d = uniform(pk.d);
     const uint32_t ncnt = (uint32_t)uniform((int)h.cnt[d]);
-#pragma unroll
-    for (int j = 0; j < kMS; ++j)
+    MC_FOR(j, mc) {
       if (((act >> j) & 1u) && af.bin(val(j)) != d) act &= ~(1u << j);
+    }
     if (ncnt == cnt) {
       active_range(act, mc, by_idx, V, xw, &vlo, &vhi);  // nothing separated: the values' own range
     } else {
@@ -1678,19 +1867,20 @@ __device__ __forceinline__ ZSel select_z(uint32_t act, const MCands& mc, double 
     cnt = ncnt;
   }
   // rank list: one LDS reservation per wave
-  const int nq = __popc(act);
+  int nq = 0;
+  MC_FOR(j, mc) { nq += (act >> j) & 1u; }
   const int qi = wave_scan_incl(nq, 0, OpAdd{});
   int rbase = 0;
   if (lane() == kWave - 1 && qi > 0) rbase = lds_fetch_add(&rl.n, qi);
   int slot = lane_value(rbase, kWave - 1) + qi - nq;
-#pragma unroll
-  for (int j = 0; j < kMS; ++j)
+  MC_FOR(j, mc) {
     if ((act >> j) & 1u) {
       rl.key[slot] = key_of(mc.z[j]);
       rl.idx[slot] = mc.idx[j];
       rl.w[slot] = MASS ? mc.w[j] : 0ull;
       ++slot;
     }
+  }
   wg_barrier();
   // lane i of every wave holds entry i; wave w compares it with entries
   // j in [8w, 8w + 8) (LDS broadcast reads) and adds its counts to the
@@ -1740,29 +1930,30 @@ __device__ __forceinline__ ZSel select_z(uint32_t act, const MCands& mc, double 
 // the first token whose running fixed-point mass exceeds floor(u * total),
 // V - 1 when none does.  The chunk holding that point comes from the
 // per-chunk kept sums (each chunk's wave sums its own); that chunk's wave
-// then locates the token alone, through index bins of the chunk's tokens
-// and the crossing bin's tokens laid out by offset.  Returns the id in the
-// lanes of the chunk's wave and -1 in the other waves.
+// then locates the token alone, through kDrawBins index bins of the chunk's
+// tokens and the crossing bin's tokens laid out by offset.  Returns the id
+// in the lanes of the chunk's wave and -1 in the other waves.
+constexpr int kDrawBins = 256;
 template <typename TIn>
 __device__ __forceinline__ int draw_chunks(const SampleArgs& a, const MCands& mc, double u, FastSmem& fs) {
   using G = Geo<TIn>;
   const int C = a.ws.C, capc = a.ws.capc, V = a.V;
-  constexpr int kTokPerBin = G::kChunk / kHB;  // 16 (float) or 8 (double) tokens per index bin
-  static_assert(kTokPerBin <= kDrawSpanMax, "span");
+  constexpr int kTokPerBin = G::kChunk / kDrawBins;  // 64 (float) or 32 (double) tokens per index bin
+  static_assert(kTokPerBin <= kWave && kTokPerBin <= kDrawSpanMax, "one lane per token of a bin");
   // per-chunk kept sums: wave w posts chunks w, w + 8, ...
   const int ng = (C + kWaves - 1) / kWaves;
   for (int g = 0; g < ng; ++g) {
     uint64_t s = 0;
-#pragma unroll
-    for (int j = 0; j < kMS; ++j)
+    MC_FOR(j, mc) {
       if (mc_group(j, capc) == g) s += mc.w[j];
+    }
     s = wave_sum(s);
     const int c = wave() + kWaves * g;
     if (lane() == 0 && c < C) fs.csum[c] = s;
   }
   wg_barrier();
   // every wave: the total, and the chunk where the running mass crosses t
-  uint64_t cs = lane() < C ? fs.csum[lane()] : 0ull;  // C <= kWave
+  const uint64_t cs = lane() < C ? fs.csum[lane()] : 0ull;  // C <= kWave
   const uint64_t incl = wave_scan_incl(cs, (uint64_t)0, OpAdd{});
   const uint64_t tot = lane_value(incl, kWave - 1);
   if (tot == 0) return V - 1;
@@ -1776,43 +1967,40 @@ __device__ __forceinline__ int draw_chunks(const SampleArgs& a, const MCands& mc
   const int gstar = cstar / kWaves;
   const int c0 = cstar * G::kChunk;
   uint64_t* hb = fs.h[0].mass;  // this wave alone uses it from here on
-  for (int b = lane(); b < kHB; b += kWave) hb[b] = 0ull;
-#pragma unroll
-  for (int j = 0; j < kMS; ++j)
+  constexpr int kPer = kDrawBins / kWave;
+  static_assert(kPer == 4, "four bins per lane");
+  reinterpret_cast<ulonglong2*>(hb)[2 * lane()] = make_ulonglong2(0ull, 0ull);
+  reinterpret_cast<ulonglong2*>(hb)[2 * lane() + 1] = make_ulonglong2(0ull, 0ull);
+  MC_FOR(j, mc) {
     if (mc_group(j, capc) == gstar && mc.w[j] != 0ull) lds_add(&hb[(mc.idx[j] - c0) / kTokPerBin], mc.w[j]);
-  // lane l sums bins [16l, 16l + 16) (rotated reads spread the banks)
-  constexpr int kPer = kHB / kWave;
-  const int b0 = kPer * lane();
-  uint64_t s = 0;
-#pragma unroll
-  for (int j = 0; j < kPer; ++j) s += hb[b0 + ((j + lane()) & (kPer - 1))];
+  }
+  // lane l holds bins [4l, 4l + 4)
+  const ulonglong2 q0 = reinterpret_cast<const ulonglong2*>(hb)[2 * lane()];
+  const ulonglong2 q1 = reinterpret_cast<const ulonglong2*>(hb)[2 * lane() + 1];
+  const uint64_t bv[kPer] = {q0.x, q0.y, q1.x, q1.y};
+  const uint64_t s = (bv[0] + bv[1]) + (bv[2] + bv[3]);
   const uint64_t in2 = wave_scan_incl(s, (uint64_t)0, OpAdd{});
-  const uint64_t ex2 = before + in2 - s;
-  const uint64_t h2 = __ballot(ex2 <= t && t < before + in2);
+  const uint64_t h2 = __ballot(before + in2 - s <= t && t < before + in2);
   if (h2 == 0) return V - 1;
   const int L = __builtin_ctzll(h2);
   int bl = 0;
-  uint64_t bf = 0;
-  if (lane() == L) {
-    uint64_t run = ex2;
+  uint64_t bf = 0, run = before + in2 - s;
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const uint64_t v = hb[b0 + j];
-      if (run <= t && t < run + v) {
-        bl = b0 + j;
-        bf = run;
-      }
-      run += v;
+  for (int j = 0; j < kPer; ++j) {
+    if (run <= t && t < run + bv[j]) {
+      bl = kPer * lane() + j;
+      bf = run;
     }
+    run += bv[j];
   }
   const int b = uniform(lane_value(bl, L));
   const uint64_t bbefore = uniform(lane_value(bf, L));
   // the bin's kept tokens by offset
   if (lane() < kTokPerBin) fs.dspan[lane()] = 0ull;
-#pragma unroll
-  for (int j = 0; j < kMS; ++j)
+  MC_FOR(j, mc) {
     if (mc_group(j, capc) == gstar && mc.w[j] != 0ull && (mc.idx[j] - c0) / kTokPerBin == b)
       fs.dspan[mc.idx[j] - c0 - b * kTokPerBin] = mc.w[j];
+  }
   const uint64_t v = lane() < kTokPerBin ? fs.dspan[lane()] : 0ull;
   const uint64_t in3 = wave_scan_incl(v, (uint64_t)0, OpAdd{});
   const uint64_t h3 = __ballot(v != 0ull && bbefore + in3 - v <= t && t < bbefore + in3);
@@ -1866,8 +2054,7 @@ __device__ __forceinline__ CandOut merge_cands(const SampleArgs& a, MCands& mc, 
   const double ymax = ys(ps.zmax);
   double s = 0.0;
   uint32_t nkept = 0;
-#pragma unroll
-  for (int j = 0; j < kMS; ++j) {
+  MC_FOR(j, mc) {
     const bool k = ((act >> j) & 1u) && mc.z[j] >= z_lo;
     const double e = k ? fast_exp_neg(ys(mc.z[j]) - ymax, tab) : 0.0;
     mc.w[j] = bits_of(e);  // the weight slot holds e until S is known
@@ -1892,8 +2079,7 @@ __device__ __forceinline__ CandOut merge_cands(const SampleArgs& a, MCands& mc, 
   }
   const double invS = 1.0 / S;
   uint32_t pos = 0;
-#pragma unroll
-  for (int j = 0; j < kMS; ++j) {
+  MC_FOR(j, mc) {
     const double p = dbl_of(mc.w[j]) * invS;
     mc.w[j] = to_fx(p);
     if (p > 0.0) pos |= 1u << j;
@@ -1906,9 +2092,9 @@ __device__ __forceinline__ CandOut merge_cands(const SampleArgs& a, MCands& mc, 
     const ZSel r = select_z<true>(pos, mc, lo, ps.zmax, nk, topp_target(rp.top_p), V, fs.rl[1], fs, xw, hgen);
     if (r.giveup) return CandOut{V - 1, true, TOPK ? 0.0 : S};
     if (r.found) {
-#pragma unroll
-      for (int j = 0; j < kMS; ++j)
+      MC_FOR(j, mc) {
         if (!(mc.z[j] > r.z || (mc.z[j] == r.z && mc.idx[j] <= r.idx))) mc.w[j] = 0ull;
+      }
     }
     if (!TOPK && ps.umax > -INFINITY) {
       // the largest token left out must fall outside the nucleus
@@ -1922,11 +2108,266 @@ __device__ __forceinline__ CandOut merge_cands(const SampleArgs& a, MCands& mc, 
   return CandOut{draw_chunks<TIn>(a, mc, rp.u, fs), false, 0.0};
 }
 
+// ------------------------------------------------- top-p rows from buckets
+// Top-p rows with no top-k (sampling.py:79-90, then :94-98), from the
+// chunks' candidate buckets (write_buckets): the bucket masses of all
+// chunks, aligned on the absolute grid, give the bucket holding the cut
+// and the mass above it; only that bucket's candidates are then ordered
+// (p descending, token index ascending), and only the chunk holding the
+// inverse-CDF point has its kept candidates read again for the draw.
+// Used when the row has at most kWaves chunks: wave c handles chunk c.
+struct BktLoad {
+  uint64_t m[kBkt / kWave];  // the lane's buckets 4l .. 4l + 3 of its wave's chunk
+  uint32_t n[kBkt / kWave];
+  int hb;                    // lane c: chunk c's top bucket
+  double ym;                 // lane c: chunk c's max y
+};
+
+__device__ __forceinline__ void load_buckets(const SampleArgs& a, int row, BktLoad& bl) {
+  const int C = a.ws.C;
+  const size_t rb = (size_t)row * C;
+  constexpr int kB4 = kBkt / kWave;
+  bl.hb = INT_MIN;
+  bl.ym = -INFINITY;
+  if (lane() < C) {
+    bl.hb = a.ws.bhb[rb + lane()];
+    bl.ym = a.ws.bymax[rb + lane()];
+  }
+#pragma unroll
+  for (int j = 0; j < kB4; ++j) {
+    bl.m[j] = 0ull;
+    bl.n[j] = 0u;
+  }
+  if (wave() < C) {
+    const size_t b = (rb + wave()) * kBkt + kB4 * lane();
+    const ulonglong2 m0 = *reinterpret_cast<const ulonglong2*>(a.ws.bmass + b);
+    const ulonglong2 m1 = *reinterpret_cast<const ulonglong2*>(a.ws.bmass + b + 2);
+    const uint4 n0 = *reinterpret_cast<const uint4*>(a.ws.bcnt + b);
+    bl.m[0] = m0.x;
+    bl.m[1] = m0.y;
+    bl.m[2] = m1.x;
+    bl.m[3] = m1.y;
+    bl.n[0] = n0.x;
+    bl.n[1] = n0.y;
+    bl.n[2] = n0.z;
+    bl.n[3] = n0.w;
+  }
+}
+
+template <typename TIn>
+__device__ __forceinline__ CandOut merge_topp(const SampleArgs& a, int row, const RowParams& rp, const PartSum& ps,
+                                              const SegLoad& sg, const BktLoad& bl, FastSmem& fs, XWave& xw,
+                                              int& hgen) {
+  using G = Geo<TIn>;
+  const int C = a.ws.C, capc = a.ws.capc, V = a.V;
+  constexpr int kB4 = kBkt / kWave;
+  const double* tab = fs.exp_tab[wave()];
+  double ms[kSegPerLane], lex;
+  const SegNorm sn = seg_norm(sg, tab, ms, &lex);
+  const double invS = 1.0 / sn.S;
+  const uint64_t target = topp_target(rp.top_p);
+  // the row's top bucket and this wave's chunk (INT_MIN: a chunk without
+  // candidates)
+  const int hbt = uniform(wave_max(bl.hb));
+  if (hbt == INT_MIN) return CandOut{V - 1, true, sn.S};
+  const int c = wave();
+  const int hbc = c < C ? uniform(lane_value(bl.hb, c)) : INT_MIN;
+  const bool mine = hbc != INT_MIN;
+  const int dc = mine ? hbt - hbc : 0;  // the chunk's bucket lb is row bucket dc + lb (the last one open)
+  // probability of a candidate of this chunk: e * Fc
+  const double Fc = mine ? fast_exp_neg(uniform(lane_value(bl.ym, c)) - sn.ymax, tab) * invS : 0.0;
+  // bucket masses in units of 2^-62 of probability, added into the row buckets
+  // (zeroed at the kernel's start)
+  wg_barrier();
+  uint64_t wv[kB4];
+#pragma unroll
+  for (int j = 0; j < kB4; ++j) {
+    wv[j] = bl.m[j] != 0ull ? (uint64_t)__double2ull_rn((double)bl.m[j] * (Fc * 1024.0)) : 0ull;
+    if (wv[j] != 0ull) {
+      const int r = min(dc + kB4 * lane() + j, kBkt - 1);
+      lds_add(&fs.rowm[r], wv[j]);
+    }
+  }
+  wg_barrier();
+  // every wave: the row bucket where the running mass from the top reaches target
+  uint64_t rv[kB4], rs = 0;
+  {
+    const ulonglong2 q0 = reinterpret_cast<const ulonglong2*>(fs.rowm)[2 * lane()];
+    const ulonglong2 q1 = reinterpret_cast<const ulonglong2*>(fs.rowm)[2 * lane() + 1];
+    rv[0] = q0.x;
+    rv[1] = q0.y;
+    rv[2] = q1.x;
+    rv[3] = q1.y;
+    rs = (rv[0] + rv[1]) + (rv[2] + rv[3]);
+  }
+  const uint64_t rin = wave_scan_incl(rs, (uint64_t)0, OpAdd{});
+  const uint64_t hx = __ballot(rin - rs < target && rin >= target);
+  if (hx == 0ull) return CandOut{V - 1, true, sn.S};
+  const int lx = __builtin_ctzll(hx);
+  int rl_ = 0;
+  uint64_t ab = 0, run = rin - rs;
+#pragma unroll
+  for (int j = 0; j < kB4; ++j) {
+    if (run < target && run + rv[j] >= target) {
+      rl_ = kB4 * lane() + j;
+      ab = run;
+    }
+    run += rv[j];
+  }
+  const int rstar = uniform(lane_value(rl_, lx));
+  const uint64_t A = uniform(lane_value(ab, lx));
+  // this chunk: mass above the cut bucket, and the list range of its
+  // candidates in the cut bucket
+  uint64_t above = 0;
+  uint32_t cnt_before = 0, cnt_in = 0;
+#pragma unroll
+  for (int j = 0; j < kB4; ++j) {
+    const int r = min(dc + kB4 * lane() + j, kBkt - 1);
+    if (r < rstar) {
+      above += wv[j];
+      cnt_before += bl.n[j];
+    } else if (r == rstar) {
+      cnt_in += bl.n[j];
+    }
+  }
+  above = wave_sum(above);
+  const int p0 = uniform(wave_sum((int)cnt_before));
+  const int p1 = p0 + uniform(wave_sum((int)cnt_in));
+  // the cut bucket's candidates of this chunk: p = e * Fc
+  MCands mc;
+  mc.valid = 0;
+  mc.jm = 0;
+  const size_t cb = ((size_t)row * C + c) * capc;
+#pragma unroll
+  for (int j = 0; j < kMS; ++j) {
+    mc.z[j] = 0.0;
+    mc.w[j] = 0ull;
+    mc.idx[j] = 0;
+    const int pos = p0 + kWave * j + lane();
+    if (mine && p0 + kWave * j < p1) {
+      mc.jm |= 1u << j;
+      if (pos < p1) {
+        const double p = a.ws.cz[cb + pos] * Fc;
+        mc.z[j] = p;
+        mc.w[j] = to_fx(p);
+        mc.idx[j] = a.ws.ci[cb + pos];
+        mc.valid |= 1u << j;
+      }
+    }
+  }
+  if (lane() == 0 && c < C) {
+    fs.cq0[c] = mine ? p0 : 0;
+    fs.cq1[c] = mine ? p1 : 0;
+  }
+  // the cut among them, in (p desc, index asc) order (select_z orders by its
+  // values, here p), starting from the mass above the bucket
+  wg_barrier();
+  uint32_t nx = 0;
+  for (int k = lane(); k < C; k += kWave) nx += (uint32_t)(fs.cq1[k] - fs.cq0[k]);
+  nx = (uint32_t)uniform((int)wave_sum(nx));
+  // every p of the bucket lies in [exp(B / 8 - ymax), exp((B + 1) / 8 - ymax)] / S
+  // (B = hbt - rstar; the last bucket is open below), with some slack
+  const double yb = (double)(hbt - rstar) / kBktPerY - sn.ymax;
+  const double plo = rstar == kBkt - 1 ? 0.0 : fast_exp_neg(yb, tab) * invS * (1.0 - 1e-9);
+  const double phi = fast_exp_neg(fmin(yb + 1.0 / kBktPerY, 0.0), tab) * invS * (1.0 + 1e-9);
+  const ZSel r = select_z<true>(mc.valid, mc, plo, phi, nx, target, V, fs.rl[1], fs, xw, hgen, A);
+  if (!r.found) return CandOut{V - 1, true, sn.S};
+  if (ps.umax > -INFINITY) {
+    // the largest token left out must fall outside the nucleus
+    const YScale ys{rp.T, 1.0 / rp.T};
+    const double pU = fast_exp_neg(ys(ps.umax) - sn.ymax, tab) * invS;
+    if (!(r.z > pU)) return CandOut{V - 1, true, sn.S};
+  }
+  // kept mass of each chunk: above the cut bucket, and its kept candidates in it
+  uint64_t kx = 0;
+  MC_FOR(j, mc) {
+    if (((mc.valid >> j) & 1u) && (mc.z[j] > r.z || (mc.z[j] == r.z && mc.idx[j] <= r.idx))) kx += mc.w[j];
+  }
+  kx = wave_sum(kx);
+  if (lane() == 0 && c < C) fs.csum[c] = mine ? above + kx : 0ull;
+  for (int b = threadIdx.x; b < kDrawBins; b += kThreads) fs.h[0].mass[b] = 0ull;
+  if (threadIdx.x < G::kChunk / kDrawBins) fs.dspan[threadIdx.x] = 0ull;
+  wg_barrier();
+  // every wave: the chunk holding the inverse-CDF point
+  const uint64_t cs = lane() < C ? fs.csum[lane()] : 0ull;
+  const uint64_t incl = wave_scan_incl(cs, (uint64_t)0, OpAdd{});
+  const uint64_t tot = lane_value(incl, kWave - 1);
+  if (tot == 0) return CandOut{V - 1, false, 0.0};
+  const uint64_t t = (uint64_t)__double2ull_rd(rp.u * (double)tot);
+  const uint64_t hc = __ballot(incl - cs <= t && t < incl && lane() < C);
+  if (hc == 0) return CandOut{V - 1, false, 0.0};
+  const int cstar = __builtin_ctzll(hc);
+  const uint64_t before = uniform(lane_value(incl - cs, cstar));
+  // its kept candidates (every thread: list positions tid, tid + 512), by
+  // index bins of the chunk's tokens
+  const double Fs = fast_exp_neg(uniform(lane_value(bl.ym, cstar)) - sn.ymax, tab) * invS;
+  // the chunk's cut-bucket range: entries before q0 are above the cut bucket
+  const int q0 = uniform(fs.cq0[cstar]);
+  const int q1 = uniform(fs.cq1[cstar]);
+  const size_t sb = ((size_t)row * C + cstar) * capc;
+  const int c0 = cstar * G::kChunk;
+  constexpr int kTokPerBin = G::kChunk / kDrawBins;
+  constexpr int kPer = kCapChunk / kThreads;
+  uint64_t dw[kPer];
+  int di[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int pos = (int)threadIdx.x + k * kThreads;
+    dw[k] = 0ull;
+    di[k] = c0;
+    if (pos < q1) {
+      const double p = a.ws.cz[sb + pos] * Fs;
+      const int id = a.ws.ci[sb + pos];
+      const bool keep = pos < q0 || p > r.z || (p == r.z && id <= r.idx);
+      dw[k] = keep ? to_fx(p) : 0ull;
+      di[k] = id;
+      if (dw[k] != 0ull) lds_add(&fs.h[0].mass[(id - c0) / kTokPerBin], dw[k]);
+    }
+  }
+  wg_barrier();
+  // every wave: the index bin, then its tokens by offset
+  const ulonglong2 b0 = reinterpret_cast<const ulonglong2*>(fs.h[0].mass)[2 * lane()];
+  const ulonglong2 b1 = reinterpret_cast<const ulonglong2*>(fs.h[0].mass)[2 * lane() + 1];
+  const uint64_t bv[4] = {b0.x, b0.y, b1.x, b1.y};
+  const uint64_t bs = (bv[0] + bv[1]) + (bv[2] + bv[3]);
+  const uint64_t bin = wave_scan_incl(bs, (uint64_t)0, OpAdd{});
+  const uint64_t hb2 = __ballot(before + bin - bs <= t && t < before + bin);
+  if (hb2 == 0) return CandOut{V - 1, false, 0.0};
+  const int L = __builtin_ctzll(hb2);
+  int bsel = 0;
+  uint64_t bf = 0, rr = before + bin - bs;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (rr <= t && t < rr + bv[j]) {
+      bsel = 4 * lane() + j;
+      bf = rr;
+    }
+    rr += bv[j];
+  }
+  const int bb = uniform(lane_value(bsel, L));
+  const uint64_t bbefore = uniform(lane_value(bf, L));
+#pragma unroll
+  for (int k = 0; k < kPer; ++k)
+    if (dw[k] != 0ull && (di[k] - c0) / kTokPerBin == bb) fs.dspan[di[k] - c0 - bb * kTokPerBin] = dw[k];
+  wg_barrier();
+  if (wave() != 0) return CandOut{-1, false, 0.0};
+  const uint64_t v = lane() < kTokPerBin ? fs.dspan[lane()] : 0ull;
+  const uint64_t in3 = wave_scan_incl(v, (uint64_t)0, OpAdd{});
+  const uint64_t h3 = __ballot(v != 0ull && bbefore + in3 - v <= t && t < bbefore + in3);
+  if (h3 == 0) return CandOut{V - 1, false, 0.0};
+  return CandOut{c0 + bb * kTokPerBin + __builtin_ctzll(h3), false, 0.0};
+}
+
 template <typename TIn, bool VEC, bool NUC>
 __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   __shared__ SmemAll sm;
   FastSmem& fs = sm.f;
   const int row = blockIdx.x;
+  // the first 128 candidate slots of each chunk (all a top-k row usually
+  // fills), read while the row's parameters are on their way
+  MCands mc;
+  const int sfirst = min(128, a.ws.capc);
+  mc_load_first(a, row, mc, sfirst);
   const RowParams rp = load_row_params(a, row);
   init_exp_table_wave(fs.exp_tab[wave()]);
   const bool cands = !rp.greedy && (rp.topk || (rp.topp && !(NUC && rp.nucleus)));
@@ -1936,6 +2377,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
       fs.h[0].mass[b] = 0ull;
     }
     if (threadIdx.x < kDrawSpanMax) fs.dspan[threadIdx.x] = 0ull;
+    if (threadIdx.x < kBkt) fs.rowm[threadIdx.x] = 0ull;
     if (threadIdx.x < 2) fs.rl[threadIdx.x].n = 0;
     if (threadIdx.x < 2 * kWave) {
       fs.rl[threadIdx.x / kWave].rank[threadIdx.x % kWave] = 0u;
@@ -1944,19 +2386,22 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   }
   XWave xw{fs.xw, 0};
   int hgen = 0;
-  // global loads first: candidates (top-p rows: every slot, their chunks
-  // fill nearly all; top-k rows: the first 128 of each chunk), segment
-  // partials, then the wave parts; a top-k chunk with more candidates is
-  // read once the counts are in
-  MCands mc;
-  const int smax = rp.topk ? min(128, a.ws.capc) : a.ws.capc;
-  if (cands) mc_load_first(a, row, mc, smax);
+  // global loads first: the rest of the candidates (top-p rows: every
+  // slot, their chunks fill nearly all), segment partials, then the wave
+  // parts; a top-k chunk with more than 128 candidates is read once the
+  // counts are in
+  // top-p rows with at most kWaves chunks: their chunks' buckets instead
+  const bool bkt = cands && !rp.topk && a.ws.C <= kWaves;
+  BktLoad bl;
+  if (bkt) load_buckets(a, row, bl);
+  const int smax = rp.topk ? sfirst : a.ws.capc;
+  if (cands && !bkt && smax > sfirst) mc_load_range(a, row, mc, sfirst, smax);
   SegLoad sg;
   if (!rp.greedy && !rp.topk && !(NUC && rp.nucleus)) {  // nucleus rows only set their bin range here
     load_segs(a, row, (a.V + Geo<TIn>::kSeg - 1) / Geo<TIn>::kSeg, sg);
   }
   const PartSum ps = scan_parts(a, row, rp.greedy, cands, fs);
-  if (cands) mc_validate(a, row, mc, fs.wcnt[wave()], smax);
+  if (cands && !bkt) mc_validate(a, row, mc, fs.wcnt[wave()], smax);
   // a chunk that could not keep all its penalised tokens aside sends the
   // row to the general pipeline
   bool general = ps.flags != 0;
@@ -1997,6 +2442,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
     id = finish_temp<TIn>(a, row, rp, sg, fs, xw);
   } else {
     const CandOut o = rp.topk ? merge_cands<TIn, true>(a, mc, sg, rp, ps, fs, xw, hgen)
+                      : bkt   ? merge_topp<TIn>(a, row, rp, ps, sg, bl, fs, xw, hgen)
                               : merge_cands<TIn, false>(a, mc, sg, rp, ps, fs, xw, hgen);
     general = o.general;
     if (!general) {
@@ -2622,7 +3068,8 @@ size_t fast_ws_bytes(int B, int V, bool f64) {
   return up256(n * kWaves * sizeof(WavePart)) + 2 * up256(n * kWaves * sizeof(double)) + up256(n * cap * sizeof(double)) +
          up256(n * cap * sizeof(int32_t)) + up256((size_t)B * sizeof(NucRow)) +
          up256((size_t)B * kNucBins * sizeof(uint32_t)) + up256(n * kWaves * sizeof(double)) + up256(n * sizeof(int32_t)) +
-         up256(n * kNucPenWords * sizeof(uint32_t));
+         up256(n * kNucPenWords * sizeof(uint32_t)) + up256(n * kBkt * sizeof(uint64_t)) +
+         up256(n * kBkt * sizeof(uint32_t)) + up256(n * sizeof(double)) + up256(n * sizeof(int32_t));
 }
 
 ChunkWs fast_ws_layout(void* base, int B, int V, bool f64) {
@@ -2650,6 +3097,14 @@ ChunkWs fast_ws_layout(void* base, int B, int V, bool f64) {
   w.ncand = reinterpret_cast<int32_t*>(p);
   p += up256(n * sizeof(int32_t));
   w.npen = reinterpret_cast<uint32_t*>(p);
+  p += up256(n * kNucPenWords * sizeof(uint32_t));
+  w.bmass = reinterpret_cast<uint64_t*>(p);
+  p += up256(n * kBkt * sizeof(uint64_t));
+  w.bcnt = reinterpret_cast<uint32_t*>(p);
+  p += up256(n * kBkt * sizeof(uint32_t));
+  w.bymax = reinterpret_cast<double*>(p);
+  p += up256(n * sizeof(double));
+  w.bhb = reinterpret_cast<int32_t*>(p);
   return w;
 }
 
