@@ -234,6 +234,22 @@ class Context:
         host = np.ascontiguousarray(host)
         return self.scratch(name, host.shape, host.dtype).upload(host)
 
+    def upload_rows(self, name: str, host: np.ndarray) -> tuple[DeviceArray, int]:
+        """Upload [N, V] rows with the row stride padded to 16 bytes, so the
+        sampling kernels take their 128-bit load path for any V (a 50 257-
+        token vocabulary included).  Returns the buffer and the stride in
+        elements; the pad columns are zero and never read."""
+        host = np.asarray(host)
+        n, v = host.shape
+        es = host.dtype.itemsize
+        ld = -(-v * es // 16) * 16 // es
+        if ld != v:
+            pad = np.empty((n, ld), host.dtype)
+            pad[:, :v] = host
+            pad[:, v:] = 0
+            host = pad
+        return self.scratch_upload(name, host), ld
+
     def pinned(self, name: str, nbytes: int) -> np.ndarray:
         """A reusable page-locked host buffer (uint8, at least nbytes), for
         plh_h2d_async; grown on demand."""

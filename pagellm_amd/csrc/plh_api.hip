@@ -4,7 +4,6 @@
 #include <string.h>
 
 #include <array>
-#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -26,8 +25,12 @@ struct plh_ctx {
   size_t ws_bytes = 0;
   hipEvent_t ws_done = nullptr;
   hipStream_t ws_stream = nullptr;
-  // plh_sample_noalloc: this device's copy of the file-scope scratch array
+  // plh_sample_noalloc: this device's copy of the file-scope scratch array;
+  // scratch_done marks the end of this context's last noalloc call (on
+  // scratch_stream)
   void* scratch = nullptr;
+  hipEvent_t scratch_done = nullptr;
+  hipStream_t scratch_stream = nullptr;
   // PLH_OPT_KERNEL_TIMING: event triples (start, between, end) per timed call
   bool timing = false;
   std::vector<hipEvent_t> ev_free;
@@ -113,7 +116,6 @@ int timing_begin(plh_ctx* c, std::array<hipEvent_t, 3>& ev) {
 }
 
 constexpr size_t kScratchBytes = size_t(64) << 20;  // the no-allocation entry point's workspace, per GPU
-constexpr int kMaxDevices = 64;
 
 }  // namespace
 
@@ -126,21 +128,28 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
 
-std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
-
 // Called by plh_create with the context's device current: the device
-// address of this device's scratch array, looked up once per device.
+// address of this device's scratch array, looked up afresh for every
+// context (a reloaded code object gets a new address).
 int resolve_scratch(plh_ctx* c) {
-  if (c->device >= kMaxDevices) return fail(c, PLH_ERR_UNSUPPORTED, "device ordinal above 63%s");
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (g_scratch_ptr[c->device] == nullptr) {
-    void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || p == nullptr) return hip_fail(c, e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
-    g_scratch_ptr[c->device] = p;
-  }
-  c->scratch = g_scratch_ptr[c->device];
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || p == nullptr) return hip_fail(c, e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+  c->scratch = p;
+  return PLH_OK;
+}
+
+// Orders a noalloc call after this context's previous one when the stream
+// changed in between: outside graph capture the new stream waits on the
+// event that closed the last call; under capture a stream change is
+// refused (a captured wait on an outside event is not allowed).
+int order_scratch(plh_ctx* c) {
+  if (c->scratch_stream == nullptr || c->scratch_stream == c->stream) return PLH_OK;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  PLH_HIP(c, hipStreamIsCapturing(c->stream, &st), "hipStreamIsCapturing");
+  if (st != hipStreamCaptureStatusNone)
+    return fail(c, PLH_ERR_INVALID_ARG, "plh_sample_noalloc: the stream changed since the last call while capturing%s");
+  PLH_HIP(c, hipStreamWaitEvent(c->stream, c->scratch_done, 0), "hipStreamWaitEvent");
   return PLH_OK;
 }
 
@@ -167,6 +176,8 @@ int sample_impl(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, in
   int rc = use_device(c);
   if (rc != PLH_OK) return rc;
   const size_t esize = dtype == PLH_F64 ? 8 : 4;
+  if ((reinterpret_cast<uintptr_t>(logits) % esize) != 0)
+    return fail(c, PLH_ERR_INVALID_ARG, "logits must be aligned to their element size%s");
   const bool vec = aligned16(logits) && ((size_t)ld * esize) % 16 == 0;
   plh::SampleArgs a{};
   a.logits = logits;
@@ -200,9 +211,13 @@ int sample_impl(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, in
                kScratchBytes);
       return fail(c, PLH_ERR_INVALID_ARG, msg);
     }
+    rc = order_scratch(c);
+    if (rc != PLH_OK) return rc;
     a.ws = plh::fast_ws_layout(c->scratch, B, V, f64);
     const hipError_t e = plh::launch_sample_fast(a, f64, vec, c->num_cu, c->stream, nullptr);
     if (e != hipSuccess) return hip_fail(c, e, "plh_sample_noalloc launch");
+    PLH_HIP(c, hipEventRecord(c->scratch_done, c->stream), "hipEventRecord");
+    c->scratch_stream = c->stream;
     return PLH_OK;
   }
   rc = reserve_ws(c, need);
@@ -242,6 +257,7 @@ int plh_create(plh_ctx** out, int device) {
     if (hipMalloc(&c->fallback, sizeof(unsigned long long)) != hipSuccess) { rc = PLH_ERR_OUT_OF_MEMORY; break; }
     if (hipMemset(c->fallback, 0, sizeof(unsigned long long)) != hipSuccess) { rc = PLH_ERR_HIP; break; }
     if (hipEventCreateWithFlags(&c->ws_done, hipEventDisableTiming) != hipSuccess) { rc = PLH_ERR_HIP; break; }
+    if (hipEventCreateWithFlags(&c->scratch_done, hipEventDisableTiming) != hipSuccess) { rc = PLH_ERR_HIP; break; }
     if (hipDeviceGetAttribute(&c->num_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
         c->num_cu <= 0) { rc = PLH_ERR_HIP; break; }
     rc = resolve_scratch(c);
@@ -261,6 +277,7 @@ void plh_destroy(plh_ctx* c) {
   if (c->ws_stream != nullptr) (void)hipStreamSynchronize(c->ws_stream);
   if (c->ws != nullptr) (void)hipFree(c->ws);
   if (c->ws_done != nullptr) (void)hipEventDestroy(c->ws_done);
+  if (c->scratch_done != nullptr) (void)hipEventDestroy(c->scratch_done);
   for (auto& t : c->ev_pending)
     for (hipEvent_t e : t) c->ev_free.push_back(e);
   for (hipEvent_t e : c->ev_free) (void)hipEventDestroy(e);
@@ -437,8 +454,19 @@ int plh_penalize(plh_ctx* c, const void* x, int dtype, int64_t ld, int B, int V,
     const uintptr_t x0 = reinterpret_cast<uintptr_t>(x), o0 = reinterpret_cast<uintptr_t>(out);
     const uintptr_t x1 = x0 + ((size_t)(B - 1) * (size_t)ld + (size_t)V) * es;
     const uintptr_t o1 = o0 + ((size_t)(B - 1) * (size_t)out_ld + (size_t)V) * es;
-    if (x0 < o1 && o0 < x1)
-      return fail(c, PLH_ERR_INVALID_ARG, "out must not overlap x (the penalty works on a copy)%s");
+    bool overlap = x0 < o1 && o0 < x1;
+    if (overlap && ld == out_ld) {
+      // interleaved rows (x = buf[:, :V], out = buf[:, V:2V]) never touch:
+      // row b' of out meets row b of x iff |d + (b' - b) * L| < V * es, with
+      // d = o0 - x0 and L the row pitch; only the two m = b' - b nearest
+      // -d / L can satisfy it
+      const int64_t d = (int64_t)(o0 - x0), L = ld * (int64_t)es, w = (int64_t)V * (int64_t)es;
+      const int64_t q = d >= 0 ? -(d / L) - 1 : (-d) / L;  // floor(-d / L) or one below it
+      overlap = false;
+      for (int64_t m = q - 1; m <= q + 2; ++m)
+        if (m > -(int64_t)B && m < (int64_t)B && d + m * L < w && d + m * L > -w) overlap = true;
+    }
+    if (overlap) return fail(c, PLH_ERR_INVALID_ARG, "out must not overlap x (the penalty works on a copy)%s");
   }
   int rc = use_device(c);
   if (rc != PLH_OK) return rc;

@@ -146,15 +146,19 @@ struct YScale {
 
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef double d2_t __attribute__((ext_vector_type(2)));
+typedef float f4u_t __attribute__((ext_vector_type(4))) __attribute__((aligned(4)));
+typedef double d2u_t __attribute__((ext_vector_type(2))) __attribute__((aligned(8)));
 template <typename TIn>
 struct VecOf;
 template <>
 struct VecOf<float> {
   typedef f4_t T;
+  typedef f4u_t U;  // the same vector at element alignment
 };
 template <>
 struct VecOf<double> {
   typedef d2_t T;
+  typedef d2u_t U;
 };
 
 // Penalised tokens a wave keeps aside (their exact float64 value); a wave
@@ -277,13 +281,21 @@ template <typename TIn, bool VEC>
 __device__ __forceinline__ void load_chunk(const TIn* x, int V, int c0, typename VecOf<TIn>::T (&v)[kU]) {
   using G = Geo<TIn>;
   using VT = typename VecOf<TIn>::T;
+  using UT = typename VecOf<TIn>::U;
   const int off = c0 + wave() * G::kSeg + lane() * G::kVW;
-  const bool full = VEC && c0 + G::kChunk <= V;  // uniform: no bounds checks needed
+  const bool full = c0 + G::kChunk <= V;  // uniform: no bounds checks needed
 #pragma unroll
   for (int j = 0; j < kU; ++j) {
     const int p = off + j * G::kSpan;
-    if (full || (VEC && p + G::kVW <= V)) {
-      v[j] = __builtin_nontemporal_load(reinterpret_cast<const VT*>(x + p));
+    if (full || p + G::kVW <= V) {
+      // 128-bit loads; rows that do not start on 16 bytes load at element
+      // alignment (dword-aligned multi-dword loads are legal on gfx9 and
+      // cost at most one extra cache line per wave load)
+      if (VEC) {
+        v[j] = __builtin_nontemporal_load(reinterpret_cast<const VT*>(x + p));
+      } else {
+        v[j] = __builtin_nontemporal_load(reinterpret_cast<const UT*>(x + p));
+      }
     } else {
 #pragma unroll
       for (int s = 0; s < G::kVW; ++s) v[j][s] = (p + s < V) ? x[p + s] : (TIn)(-INFINITY);
@@ -409,8 +421,8 @@ __device__ __forceinline__ bool set_aside_penalised(ChunkToks<TIn>& tk, uint32_t
 
 // Histogram bins of the register tokens in their input precision: the
 // bounds of a float64 Affine rounded to float (lo rounded down) for float
-// inputs.  Rounding in the float arithmetic moves a bin edge by at most
-// 2^-23 * 1024 bins, well inside the 0.01-bin margin of the threshold.
+// inputs.  margin() is how far, in bins, rounding can move a bin edge; the
+// threshold taken from a bin backs off by it.
 template <typename TIn>
 struct InAffine {
   Affine af;
@@ -418,6 +430,7 @@ struct InAffine {
   __device__ __forceinline__ int bin(TIn x) const { return af.bin(x); }
   __device__ __forceinline__ double lo() const { return af.lo; }
   __device__ __forceinline__ double scale() const { return af.scale; }
+  __device__ __forceinline__ double margin() const { return 0.01; }
 };
 template <>
 struct InAffine<float> {
@@ -430,17 +443,17 @@ struct InAffine<float> {
     off_f = -lo_f * scale_f;
   }
   // finite x >= lo_f: x * scale - lo * scale in one fma, clamped to
-  // [0, nb - 1] by the median.  Rounding moves a bin edge by ~2^-24 of
-  // |lo| * scale bins: well inside the threshold's 0.01-bin margin for
-  // logits of ordinary range.  Far outside it, a bin holds a few tokens
-  // too many or too few; the candidate test (x >= theta) and the bound
-  // (theta) stay exact, so that changes only how many candidates a chunk
-  // keeps.
+  // [0, nb - 1] by the median.  The rounded off_f moves every bin edge by
+  // up to |off_f| * 2^-24 bins and the fma's own rounding adds up to
+  // nb * 2^-24: with logits of ordinary range well inside 0.01 bin, but
+  // far from zero (logits near 1e4 over a narrow chunk range) it can reach
+  // a tenth of a bin, so margin() grows with |off_f|.
   __device__ __forceinline__ int bin(float x) const {
     return (int)__builtin_amdgcn_fmed3f(fmaf(x, scale_f, off_f), 0.0f, (float)(nb - 1));
   }
   __device__ __forceinline__ double lo() const { return (double)lo_f; }
   __device__ __forceinline__ double scale() const { return (double)scale_f; }
+  __device__ __forceinline__ double margin() const { return 0.01 + ((double)fabsf(off_f) + nb) * 0x1p-22; }
 };
 
 // The smallest input-precision value >= theta (every finite value when theta
@@ -689,12 +702,13 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
   if (hi > -INFINITY) {
     const Affine af = make_affine(lo, hi, kHB);
     const InAffine<TIn> rf(af);
-    double tlo = af.lo, tscale = af.scale;
+    double tlo = af.lo, tscale = af.scale, tmargin = 0.01;
     if (by_max) {
       if (lmax > -INFINITY) lds_add(&cm.hcnt[af.bin(lmax)], 1u);
     } else {
       tlo = rf.lo();
       tscale = rf.scale();
+      tmargin = rf.margin();
       const Affine pf{tlo, tscale, kHB};  // the same bins in float64, for the penalised tokens
       const TIn lin = in_threshold<TIn>(lo);
       uint32_t one = 1u;  // kept in a register, not rematerialised for every slot
@@ -712,9 +726,9 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
     }
     wg_barrier();
     const int d = hist_reach_desc(cm.hcnt, (uint32_t)target);
-    // every z with bin(z) >= d is >= lo + (d - 0.01) / scale (bin(z) is
+    // every z with bin(z) >= d is >= lo + (d - margin) / scale (bin(z) is
     // floor((z - lo) * scale) up to rounding); bin 0 starts at lo
-    if (d >= 0) theta = d > 0 ? tlo + ((double)d - 0.01) / tscale : lo;
+    if (d >= 0) theta = d > 0 ? tlo + ((double)d - tmargin) / tscale : lo;
   }
   theta = uniform(theta);
   const TIn tin = in_threshold<TIn>(theta);

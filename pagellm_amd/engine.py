@@ -178,8 +178,8 @@ class BatchSampler:
             if host.ndim != 2 or host.shape[0] != B:
                 raise ValueError("logits must be [B, V]")
             V = host.shape[1]
-            dev = c.scratch_upload("eng_logits", host)
-            ptr, ld, code = dev.ptr, V, _native.dtype_code(host.dtype)
+            dev, ld = c.upload_rows("eng_logits", host)
+            ptr, code = dev.ptr, _native.dtype_code(host.dtype)
             c.set_stream(None)
         if V != self.hist.V:
             raise ValueError(f"vocabulary {V} does not match the histories' {self.hist.V}")

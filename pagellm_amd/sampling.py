@@ -213,8 +213,8 @@ def sample_batch(
         B, V = host.shape
         if B and V == 0:
             raise ValueError("empty vocabulary")
-        dev = c.scratch_upload("logits", host)
-        ptr, ld, code = dev.ptr, V, _native.dtype_code(host.dtype)
+        dev, ld = c.upload_rows("logits", host)
+        ptr, code = dev.ptr, _native.dtype_code(host.dtype)
         c.set_stream(None)
     if B == 0:
         return np.zeros(0, dtype=np.int64)

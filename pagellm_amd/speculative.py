@@ -150,11 +150,11 @@ def _probs_rows(c, x: np.ndarray, dev, hist, tag: str):
     Returns (ids int32 [N] on the device, probs float64 [N, V] on the
     device)."""
     N, V = x.shape
-    d_x = c.scratch_upload(f"{tag}_x", x)
+    d_x, ld = c.upload_rows(f"{tag}_x", x)
     out = c.scratch(f"{tag}_out", (N,), np.int32)
     probs = c.scratch(f"{tag}_probs", (N, V), np.float64)
     h_ids, h_off, flags = hist if hist is not None else (None, None, 0)
-    c.sample(d_x.ptr, _native.dtype_code(x.dtype), V, N, V, h_ids, h_off, *dev, out.ptr, probs.ptr, flags)
+    c.sample(d_x.ptr, _native.dtype_code(x.dtype), ld, N, V, h_ids, h_off, *dev, out.ptr, probs.ptr, flags)
     return out, probs
 
 

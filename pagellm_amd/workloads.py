@@ -93,9 +93,11 @@ MIXED_GROUPS = (
 )
 
 
-def mixed128k(rows: int = 256):
+def mixed128k(rows: int = 256, V: int = 128256):
+    """The mixed-parameter batch (N(0, 3^2) logits plus 8 spikes of +10 a
+    row, four parameter groups); V other than 128 256 gives the same recipe
+    at another vocabulary size."""
     g = np.random.default_rng(1003)
-    V = 128256
     logits = g.normal(0.0, 3.0, (rows, V)).astype(np.float32)
     for b in range(rows):
         logits[b, g.choice(V, 8, replace=False)] += np.float32(10.0)

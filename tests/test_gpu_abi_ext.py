@@ -10,6 +10,7 @@ import pytest
 
 import oracle
 from pagellm_amd import _native
+from parity import DRAW_GAP, TOPP_GAP
 from pagellm_amd.params import SamplingParams
 from pagellm_amd.sampling import _pack_params
 
@@ -108,7 +109,7 @@ def test_quantized_logits_general_path():
         ref = oracle.sample(x[b], params[b], u[b], ())
         if ids[b] != ref:
             gt, gd = sample_boundary_gaps(x[b], params[b], u[b], ())
-            assert gt < 1e-12 or gd < 1e-6, (b, int(ids[b]), ref)
+            assert gt < TOPP_GAP or gd < DRAW_GAP, (b, int(ids[b]), ref)
     c.close()
 
 
@@ -166,7 +167,7 @@ def test_nucleus_hint_changes_the_path_not_the_ids():
                                           _native.PLH_SAMPLE_NUCLEUS | _native.PLH_SAMPLE_HIST_SPANS))
     for b in range(B):
         ref = oracle.sample(x[b], params[b], u[b], hists[b])
-        assert hinted[b] == ref or min(oracle.sampler.sample_boundary_gaps(x[b], params[b], u[b], hists[b])) < 1e-6
+        assert hinted[b] == ref or min(oracle.sampler.sample_boundary_gaps(x[b], params[b], u[b], hists[b])) < DRAW_GAP
 
 
 def test_penalize_rejects_in_place_and_overlapping_output():
@@ -192,3 +193,12 @@ def test_penalize_rejects_in_place_and_overlapping_output():
     assert np.array_equal(got[0], oracle.apply_repetition_penalty(x[0], ids.tolist(), 1.5))
     assert np.array_equal(got[1], x[1])
     assert np.array_equal(d_x.download(), x)  # the input is untouched
+    # interleaved rows of one buffer never touch: x = buf[:, :V], out = buf[:, V:2V]
+    buf = np.concatenate([x, np.zeros_like(x)], axis=1)
+    d_buf = c.to_device(buf)
+    c.penalize(d_buf.ptr, _native.PLH_F32, 2 * V, B, V, d_ids.ptr, d_off.ptr, d_pen.ptr, d_buf.ptr + 4 * V, 2 * V)
+    both = d_buf.download()
+    assert np.array_equal(both[:, :V], x) and np.array_equal(both[:, V:], got)
+    with pytest.raises(ValueError, match="overlap"):  # out's row 0 reaches one element into x's row 1
+        c.penalize(d_buf.ptr, _native.PLH_F32, 2 * V, B, V, d_ids.ptr, d_off.ptr, d_pen.ptr,
+                   d_buf.ptr + 4 * (V + 1), 2 * V)

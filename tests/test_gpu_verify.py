@@ -10,6 +10,7 @@ import pytest
 import oracle
 from oracle.sampler import verify_boundary_gap
 from pagellm_amd import workloads
+from parity import BAND, DRAW_GAP
 from pagellm_amd.speculative import verify, verify_batch
 
 pytestmark = pytest.mark.gpu
@@ -22,25 +23,29 @@ def _dist(rng, V, sharp=1.0):
 
 @pytest.mark.parametrize("k", [1, 2, 3])
 def test_kat_verify_law(kats, k):
+    """The reference's law test (``test_speculative.py:14-39``) at its full
+    40 000 trials, all trials in one batched verify: the first emitted token
+    follows p[0] and, after an acceptance, the second follows p[1]."""
     c = kats["verify_law"]
     rng = np.random.default_rng(k)
     V = c["V"]
     p = np.stack([_dist(rng, V, c["sharp"]) for _ in range(k + 1)])
     q = np.stack([_dist(rng, V, c["sharp"]) for _ in range(k)])
-    trials = c["trials"] // 2
-    first = np.zeros(V)
-    joint = np.zeros((V, V))
-    n_joint = 0
-    for _ in range(trials):
-        xs = [oracle.draw(q[i], rng) for i in range(k)]
-        out, _ = verify(p, q, xs, rng)
-        first[out[0]] += 1
-        if len(out) >= 2:
-            joint[out[0], out[1]] += 1
-            n_joint += 1
+    trials = c["trials"]
+    cq = np.cumsum(q, axis=1)
+    xs = np.stack([np.minimum(np.searchsorted(cq[i], rng.random(trials) * cq[i, -1], side="right"), V - 1)
+                   for i in range(k)], axis=1)
+    au = rng.random((trials, k))
+    ru = rng.random(trials)
+    toks, n = verify_batch(np.broadcast_to(p, (trials, k + 1, V)), np.broadcast_to(q, (trials, k, V)), xs, au, ru)
+    first = np.bincount(toks[:, 0], minlength=V)
     assert 0.5 * np.abs(first / trials - p[0]).sum() < c["tv_first"]
     if k >= 2:
-        assert 0.5 * np.abs(joint.sum(0) / n_joint - p[1]).sum() < c["tv_conditional"]
+        two = n >= 1
+        second = np.bincount(toks[two, 1], minlength=V)
+        assert 0.5 * np.abs(second / two.sum() - p[1]).sum() < c["tv_conditional"]
+    rt, rn = oracle.verify_batch(p[None].repeat(256, 0), q[None].repeat(256, 0), xs[:256], au[:256], ru[:256])
+    assert np.array_equal(rn, n[:256]) and np.array_equal(rt, toks[:256])
 
 
 def test_kat_verify_identical(kats):
@@ -95,13 +100,15 @@ def test_spec32k_parity():
     w = workloads.spec32k()
     toks, n = verify_batch(w["p"], w["q"], w["draft"], w["accept_u"], w["resample_u"])
     rt, rn = oracle.verify_batch(w["p"], w["q"], w["draft"], w["accept_u"], w["resample_u"])
-    boundary = 0
+    mism = band = 0
     for b in range(len(n)):
+        gap = verify_boundary_gap(w["p"][b], w["q"][b], list(w["draft"][b]), w["accept_u"][b], w["resample_u"][b])
+        band += gap < BAND
         if n[b] != rn[b] or not np.array_equal(toks[b], rt[b]):
-            gap = verify_boundary_gap(w["p"][b], w["q"][b], list(w["draft"][b]), w["accept_u"][b], w["resample_u"][b])
-            assert gap < 1e-6, (b, gap)
-            boundary += 1
-    print(f"spec32k rows {len(n)}, accepted mean {n.mean():.3f}, boundary cases {boundary}")
+            assert gap < DRAW_GAP, (b, gap)
+            mism += 1
+    print(f"spec32k rows {len(n)}, accepted mean {n.mean():.3f}, mismatches {mism}, "
+          f"rows within 1e-6 of a decision boundary {band}")
 
 
 def test_spec32k_float32_inputs():
@@ -163,7 +170,7 @@ def test_verify_draw_across_chunks():
         for b in range(len(n)):
             if n[b] != rn[b] or not np.array_equal(toks[b], rt[b]):
                 gap = verify_boundary_gap(Pc[b], Qc[b], drafts[b], aus[b], dus[b])
-                assert gap < 1e-6, (dt, b, n[b], rn[b], gap)
+                assert gap < DRAW_GAP, (dt, b, n[b], rn[b], gap)
 
 
 def test_verify_draw_ends_of_the_cdf():
@@ -233,4 +240,4 @@ def test_random_verify_batches(seed):
         rt, rn = oracle.verify_batch(p64, q64, draft, au, ru)
         for b in np.nonzero((n != rn) | (toks != rt).any(1))[0]:
             gap = verify_boundary_gap(p64[b], q64[b], list(draft[b]), au[b], float(ru[b]))
-            assert gap < 1e-6, (it, int(b), toks[b].tolist(), rt[b].tolist(), gap)
+            assert gap < DRAW_GAP, (it, int(b), toks[b].tolist(), rt[b].tolist(), gap)

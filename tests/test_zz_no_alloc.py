@@ -15,7 +15,9 @@ from pagellm_amd.sampling import _nucleus_hint, _pack_histories, _pack_params
 pytestmark = pytest.mark.gpu
 
 
-def _call(c, w, noalloc, rows=None):
+def _launch(c, w, noalloc, rows=None):
+    """Uploads the rows and launches plh_sample(_noalloc) on the context's
+    stream; returns the device ids (not yet waited for)."""
     x = w["logits"] if rows is None else w["logits"][:rows]
     params = w["params"] if rows is None else w["params"][:rows]
     ctxs = w["contexts"] if rows is None else w["contexts"][:rows]
@@ -30,7 +32,12 @@ def _call(c, w, noalloc, rows=None):
     fn = c.sample_noalloc if noalloc else c.sample
     fn(d["x"].ptr, _native.dtype_code(x.dtype), V, B, V, hi.ptr if hi else None, ho.ptr if ho else None,
        d["t"].ptr, d["k"].ptr, d["p"].ptr, d["r"].ptr, d["u"].ptr, out.ptr, None, _nucleus_hint(t, k, p, V))
-    return out.download()
+    out.keep = (d, hi, ho)  # the inputs live as long as the output
+    return out
+
+
+def _call(c, w, noalloc, rows=None):
+    return _launch(c, w, noalloc, rows).download()
 
 
 def test_noalloc_matches_sample_on_two_calls_in_a_row():
@@ -50,6 +57,31 @@ def test_noalloc_matches_sample_on_two_calls_in_a_row():
         assert np.array_equal(got_small2, ref_small)
         assert np.array_equal(got_char, _call(c, workloads.char65(), False))
     finally:
+        c.close()
+
+
+def test_noalloc_orders_calls_on_two_streams():
+    """Back-to-back noalloc calls of one context on two streams, with no
+    host wait between them: the second waits on the first (both share the
+    GPU's scratch array), and both return plh_sample's ids."""
+    import torch
+
+    c = _native.Context(0)
+    try:
+        big = workloads.mixed128k()
+        small = workloads.zipf32k()
+        ref_big = _call(c, big, False)
+        ref_small = _call(c, small, False, rows=40)
+        s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+        c.set_stream(s1.cuda_stream)
+        o1 = _launch(c, big, True)
+        c.set_stream(s2.cuda_stream)
+        o2 = _launch(c, small, True, rows=40)
+        torch.cuda.synchronize()
+        assert np.array_equal(o1.download(), ref_big)
+        assert np.array_equal(o2.download(), ref_small)
+    finally:
+        c.set_stream(None)
         c.close()
 
 
