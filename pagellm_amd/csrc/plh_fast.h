@@ -59,25 +59,33 @@ __device__ __forceinline__ double fast_exp_neg(double d, const double* tab) {
   return ldexp(tab[k & 63] * q, k >> 6);
 }
 
-// exp(d) for d <= 0 as a term of a normaliser sum: the reduction and
-// polynomial of fast_exp_neg, with k = rint(d * 64 / ln2) from the
-// magic-number rounding (adding 1.5 * 2^52 leaves k in the low mantissa
-// bits).  d is clamped at -708, where the scaled result is still normal: a
-// term below e^-708 (including -inf) counts as e^-708 ~ 3e-308, which no
-// sum holding a term of 1 can notice.
+// exp(d) for d <= 0 as a term of a normaliser sum, relative error below
+// 3e-15 for d >= -40 (the terms a sum holding a term of 1 can notice):
+//   * k = rint(d * 64 / ln2) from the magic-number rounding (adding
+//     1.5 * 2^52 leaves k in the low mantissa bits);
+//   * r = d - k * ln2/64 with ln2/64 as one double: the constant's error,
+//     |k| * 2^-60, stays below 3.3e-15 for |k| <= 3694 (d >= -40);
+//   * exp(r) on |r| <= ln2/128 by the degree-4 polynomial interpolating exp
+//     at the five Chebyshev nodes of that interval (relative error 2.4e-15;
+//     kExpCheb4, from pagellm_amd/csrc/exp_poly.py);
+//   * times 2^(k/64) from the table, scaled by 2^(k>>6) with ldexp.
+// d is clamped at -708, where the scaled result is still normal: a term
+// below e^-708 (including -inf) counts as e^-708 ~ 3e-308, which no sum
+// holding a term of 1 can notice.
 constexpr double kExpMagic = 6755399441055744.0;  // 1.5 * 2^52
+constexpr double kLn2Over64 = 0x1.62e42fefa39efp-7;  // ln2 / 64 rounded to double
+constexpr double kExpCheb4[4] = {0x1.fffffffffb135p-1, 0x1.fffffffffe5b9p-2, 0x1.55557e54ffd7ep-3,
+                                 0x1.555570ac8d5b7p-5};  // r^1..r^4 (r^0: exactly 1)
 
 __device__ __forceinline__ double exp_neg_term(double d, const double* tab) {
   d = fmax(d, -708.0);
   const double t = fma(d, 64.0 / 0.6931471805599453, kExpMagic);
   const int k = __double2loint(t);
   const double kd = t - kExpMagic;
-  double r = fma(-kd, kLn2Hi / 64.0, d);
-  r = fma(-kd, kLn2Lo / 64.0, r);
-  double q = fma(r, 1.0 / 120.0, 1.0 / 24.0);
-  q = fma(q, r, 1.0 / 6.0);
-  q = fma(q, r, 0.5);
-  q = fma(q, r, 1.0);
+  const double r = fma(-kd, kLn2Over64, d);
+  double q = fma(r, kExpCheb4[3], kExpCheb4[2]);
+  q = fma(q, r, kExpCheb4[1]);
+  q = fma(q, r, kExpCheb4[0]);
   q = fma(q, r, 1.0);
   return ldexp(tab[k & 63] * q, k >> 6);
 }

@@ -116,6 +116,50 @@ __device__ __forceinline__ RowParams load_row_params(const SampleArgs& a, int ro
   return rp;
 }
 
+// The same parameters read with vector loads (every lane the same
+// address), so that they travel in one round trip with the other loads a
+// kernel issues before it knows the row's mode; row_params_of() makes them
+// uniform once they are in.
+struct RowLoad {
+  double T, top_p, pen, u;
+  int top_k;
+  int64_t h0, h1;
+};
+
+__device__ __forceinline__ int lane_zero() {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));  // a zero the compiler cannot see as uniform
+  return z;
+}
+
+__device__ __forceinline__ void issue_row_params(const SampleArgs& a, int row, RowLoad& rl) {
+  const int r = row + lane_zero();
+  rl.T = a.temperature[r];
+  rl.top_k = a.top_k[r];
+  rl.top_p = a.top_p[r];
+  rl.pen = a.rep_penalty[r];
+  rl.u = a.uniforms != nullptr ? a.uniforms[r] : 0.0;
+  rl.h0 = a.hist_off != nullptr ? a.hist_off[a.hist_spans ? 2 * r : r] : 0;
+  rl.h1 = a.hist_off != nullptr ? a.hist_off[a.hist_spans ? 2 * r + 1 : r + 1] : 0;
+}
+
+__device__ __forceinline__ RowParams row_params_of(const SampleArgs& a, const RowLoad& rl) {
+  RowParams rp;
+  rp.T = uniform(rl.T);
+  rp.top_k = uniform(rl.top_k);
+  rp.top_p = uniform(rl.top_p);
+  rp.pen = uniform(rl.pen);
+  rp.u = uniform(rl.u);
+  rp.h0 = (int64_t)uniform((uint64_t)rl.h0);
+  rp.h1 = (int64_t)uniform((uint64_t)rl.h1);
+  rp.greedy = rp.T == 0.0;
+  rp.pen_active = rp.pen != 1.0 && rp.h1 > rp.h0 && a.hist_ids != nullptr;
+  rp.topk = !rp.greedy && rp.top_k > 0 && rp.top_k < a.V;
+  rp.topp = !rp.greedy && rp.top_p < 1.0;
+  rp.nucleus = a.nucleus != 0 && rp.topp && !rp.topk && rp.top_p >= kNucTopP;
+  return rp;
+}
+
 template <typename TIn, bool VEC>
 __device__ __forceinline__ int row_general(const SampleArgs& a, int row, const RowParams& rp, Smem& sm,
                                            double* probs_out, PipeIn in = PipeIn{false, 0.0, false, 0.0, false, 0.0}) {
@@ -147,6 +191,8 @@ struct YScale {
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef double d2_t __attribute__((ext_vector_type(2)));
 typedef float f4u_t __attribute__((ext_vector_type(4))) __attribute__((aligned(4)));
+// word 3 of a gfx9 buffer resource for raw 32-bit accesses (DATA_FORMAT 32)
+constexpr int kBufDword3 = 0x00020000;
 typedef double d2u_t __attribute__((ext_vector_type(2))) __attribute__((aligned(8)));
 template <typename TIn>
 struct VecOf;
@@ -284,22 +330,45 @@ __device__ __forceinline__ void load_chunk(const TIn* x, int V, int c0, typename
   using UT = typename VecOf<TIn>::U;
   const int off = c0 + wave() * G::kSeg + lane() * G::kVW;
   const bool full = c0 + G::kChunk <= V;  // uniform: no bounds checks needed
+  // 128-bit loads; rows that do not start on 16 bytes load at element
+  // alignment (dword-aligned multi-dword loads are legal on gfx9 and cost
+  // at most one extra cache line per wave load)
+  if (full) {
+#pragma unroll
+    for (int j = 0; j < kU; ++j) {
+      const int p = off + j * G::kSpan;
+      if (VEC) v[j] = __builtin_nontemporal_load(reinterpret_cast<const VT*>(x + p));
+      else v[j] = __builtin_nontemporal_load(reinterpret_cast<const UT*>(x + p));
+    }
+    return;
+  }
+  // the row's last chunk: buffer loads range-checked against the row's
+  // length (V elements from x), which return 0 past it and cannot fault,
+  // with no branch between them (a branch per slot makes the compiler wait
+  // between the loads).  The vector that straddles the row's end (at most
+  // one per lane) is loaded again element by element; then the slots past
+  // the end take -inf.
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<TIn*>(x), (short)0, V * (int)sizeof(TIn), kBufDword3);
+  int ps = -1;  // start of the straddling vector
 #pragma unroll
   for (int j = 0; j < kU; ++j) {
     const int p = off + j * G::kSpan;
-    if (full || p + G::kVW <= V) {
-      // 128-bit loads; rows that do not start on 16 bytes load at element
-      // alignment (dword-aligned multi-dword loads are legal on gfx9 and
-      // cost at most one extra cache line per wave load)
-      if (VEC) {
-        v[j] = __builtin_nontemporal_load(reinterpret_cast<const VT*>(x + p));
-      } else {
-        v[j] = __builtin_nontemporal_load(reinterpret_cast<const UT*>(x + p));
-      }
-    } else {
+    v[j] = __builtin_bit_cast(VT, __builtin_amdgcn_raw_buffer_load_b128(rs, p * (int)sizeof(TIn), 0, 0));
+    if (p < V && p + G::kVW > V) ps = p;
+  }
+  TIn tl[G::kVW];
 #pragma unroll
-      for (int s = 0; s < G::kVW; ++s) v[j][s] = (p + s < V) ? x[p + s] : (TIn)(-INFINITY);
-    }
+  for (int s = 0; s < G::kVW; ++s) {
+    const int o = ps >= 0 ? (ps + s) * (int)sizeof(TIn) : INT_MAX;  // INT_MAX: out of range, reads 0
+    if constexpr (sizeof(TIn) == 4) tl[s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, o, 0, 0));
+    else tl[s] = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(rs, o, 0, 0));
+  }
+#pragma unroll
+  for (int j = 0; j < kU; ++j) {
+    const int p = off + j * G::kSpan;
+#pragma unroll
+    for (int s = 0; s < G::kVW; ++s) v[j][s] = p + s < V ? (p == ps ? tl[s] : v[j][s]) : (TIn)(-INFINITY);
   }
 }
 
@@ -837,10 +906,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   if (g < 0) return;
   const int row = g / C;
   const int c0 = (g - row * C) * G::kChunk;
-  const RowParams rp = load_row_params(a, row);
+  // the row's parameters as vector loads, in flight with the chunk's (a
+  // scalar load of them would hold the chunk's loads behind its return)
+  RowLoad rload;
+  issue_row_params(a, row, rload);
   const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
   ChunkToks<TIn> tk;
   load_chunk<TIn, VEC>(x, a.V, c0, tk.v);
+  const RowParams rp = row_params_of(a, rload);
   const bool cands = rp.topk || (rp.topp && !(NUC && rp.nucleus));
   if (cands) {  // ordered before use by the first barrier of chunk_candidates
     for (int b = threadIdx.x; b < kHB; b += kThreads) cm.hcnt[b] = 0u;
@@ -1351,7 +1424,21 @@ struct PartSum {
   ArgMax best;
 };
 
-__device__ __forceinline__ PartSum scan_parts(const SampleArgs& a, int row, bool greedy, bool cands, FastSmem& fs) {
+// The row's first kWave wave parts (all of them for V <= 8 chunks), one per
+// lane, read before the row's parameters are known.
+struct PartLoad {
+  WavePart p;
+};
+
+__device__ __forceinline__ void load_parts_first(const SampleArgs& a, int row, PartLoad& pl) {
+  // unconditional (lanes past the row's parts read its last one, unused):
+  // no branch for the compiler to pull the parts' first uses into
+  const int P = a.ws.C * kWaves;
+  pl.p = a.ws.part[(size_t)row * P + min(lane(), P - 1)];
+}
+
+__device__ __forceinline__ PartSum scan_parts(const SampleArgs& a, int row, bool greedy, bool cands, FastSmem& fs,
+                                              const PartLoad& pl) {
   const int P = a.ws.C * kWaves;
   const WavePart* pp = a.ws.part + (size_t)row * P;
   int* wc = fs.wcnt[wave()];
@@ -1360,7 +1447,7 @@ __device__ __forceinline__ PartSum scan_parts(const SampleArgs& a, int row, bool
   double um = -INFINITY, zm = -INFINITY, un = INFINITY;
   ArgMax best{-INFINITY, INT_MAX};
   for (int j = lane(); j < P; j += kWave) {
-    const WavePart& p = pp[j];
+    const WavePart p = j < kWave ? pl.p : pp[j];
     fl |= p.flags;
     if (greedy) best = argmax_merge(best, ArgMax{p.best_z, p.best_idx});
     if (cands) {
@@ -2379,10 +2466,17 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   const int row = blockIdx.x;
   // the first 128 candidate slots of each chunk (all a top-k row usually
   // fills), read while the row's parameters are on their way
+  RowLoad rload;
+  issue_row_params(a, row, rload);
   MCands mc;
   const int sfirst = min(128, a.ws.capc);
   mc_load_first(a, row, mc, sfirst);
-  const RowParams rp = load_row_params(a, row);
+  // and the row's first wave parts (every mode reads them), in the same
+  // round trip; the rest waits for the row's mode (more loads in flight at
+  // once lengthen the round trip for every row)
+  PartLoad pl;
+  load_parts_first(a, row, pl);
+  const RowParams rp = row_params_of(a, rload);
   init_exp_table_wave(fs.exp_tab[wave()]);
   const bool cands = !rp.greedy && (rp.topk || (rp.topp && !(NUC && rp.nucleus)));
   if (cands) {  // ordered before their first use by the first barrier
@@ -2400,11 +2494,9 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   }
   XWave xw{fs.xw, 0};
   int hgen = 0;
-  // global loads first: the rest of the candidates (top-p rows: every
-  // slot, their chunks fill nearly all), segment partials, then the wave
-  // parts; a top-k chunk with more than 128 candidates is read once the
-  // counts are in
-  // top-p rows with at most kWaves chunks: their chunks' buckets instead
+  // top-p rows with more than kWaves chunks read the rest of their
+  // candidates (their chunks fill nearly all slots) now; a top-k chunk
+  // with more than 128 candidates is read once the counts are in
   const bool bkt = cands && !rp.topk && a.ws.C <= kWaves;
   BktLoad bl;
   if (bkt) load_buckets(a, row, bl);
@@ -2414,7 +2506,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   if (!rp.greedy && !rp.topk && !(NUC && rp.nucleus)) {  // nucleus rows only set their bin range here
     load_segs(a, row, (a.V + Geo<TIn>::kSeg - 1) / Geo<TIn>::kSeg, sg);
   }
-  const PartSum ps = scan_parts(a, row, rp.greedy, cands, fs);
+  const PartSum ps = scan_parts(a, row, rp.greedy, cands, fs, pl);
   if (cands && !bkt) mc_validate(a, row, mc, fs.wcnt[wave()], smax);
   // a chunk that could not keep all its penalised tokens aside sends the
   // row to the general pipeline
