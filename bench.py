@@ -245,6 +245,9 @@ def pmc_probe(workload: str, group: int | None = None) -> None:
     from pagellm_amd import _native, workloads
     from pagellm_amd.sampling import _nucleus_hint, _pack_histories, _pack_params
 
+    if workload == "spec32k":
+        _pmc_probe_verify()
+        return
     w = workloads.WORKLOADS[workload]()
     B, V = w["logits"].shape
     rows = _probe_rows(workload, group, B)
@@ -264,7 +267,7 @@ def pmc_probe(workload: str, group: int | None = None) -> None:
     dst = torch.empty_like(src)
     dst.copy_(src)
     torch.cuda.synchronize()
-    for _ in range(3):
+    for _ in range(PROBE_STEPS):
         ctx.sample(x.data_ptr(), _native.PLH_F32, V, B, V,
                    d["ids"].data_ptr() if "ids" in d else None, d["off"].data_ptr() if "off" in d else None,
                    d["t"].data_ptr(), d["k"].data_ptr(), d["p"].data_ptr(), d["r"].data_ptr(),
@@ -274,9 +277,63 @@ def pmc_probe(workload: str, group: int | None = None) -> None:
     print("pmc probe done", flush=True)
 
 
+PROBE_STEPS = 3
+
+
+def _pmc_probe_verify() -> None:
+    """The counter probe of spec32k: the calibration copy, then PROBE_STEPS
+    verify calls on one set of p and q."""
+    import torch
+
+    from pagellm_amd import _native, workloads
+
+    w = workloads.spec32k()
+    B, k1, V = w["p"].shape
+    k = k1 - 1
+    dev = torch.device("cuda:0")
+    ctx = _native.Context(0)
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    d = {n: torch.from_numpy(w[n]).to(dev) for n in ("p", "q", "accept_u", "resample_u")}
+    dr = torch.from_numpy(w["draft"].astype("int32")).to(dev)
+    tok = torch.empty((B, k1), dtype=torch.int32, device=dev)
+    nacc = torch.empty(B, dtype=torch.int32, device=dev)
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    for _ in range(PROBE_STEPS):
+        ctx.verify(d["p"].data_ptr(), d["q"].data_ptr(), _native.PLH_F64, B, k, V, dr.data_ptr(),
+                   d["accept_u"].data_ptr(), d["resample_u"].data_ptr(), False, tok.data_ptr(), nacc.data_ptr())
+    torch.cuda.synchronize()
+    ctx.close()
+    print("pmc probe done", flush=True)
+
+
+def _spec32k_compulsory_bytes() -> int:
+    """Bytes one spec32k verify call must read (data dependent, from the
+    oracle's stop positions): 16 B per accept test made, then p and q of
+    the rejected position, or p_k after k acceptances (float64)."""
+    import numpy as np
+
+    from pagellm_amd import workloads
+
+    w = workloads.spec32k()
+    B, k1, V = w["p"].shape
+    k = k1 - 1
+    rows = np.arange(B)[:, None]
+    px = w["p"][rows, np.arange(k)[None, :], w["draft"]]
+    qx = w["q"][rows, np.arange(k)[None, :], w["draft"]]
+    with np.errstate(divide="ignore", invalid="ignore"):
+        ok = w["accept_u"] < np.minimum(1.0, px / qx)  # speculative.py:51-53
+    n = np.where(ok.all(axis=1), k, np.argmin(ok, axis=1))  # the first rejection, else k
+    return int(sum(16 * min(int(s) + 1, k) + (16 * V if s < k else 8 * V) for s in n))
+
+
 def traffic_from(workload: str, fetch_dir: str, write_dir: str, dst: Path | None = None) -> dict:
-    """HBM bytes per k_sample_chunks launch from the two counter runs,
-    written to profiles/traffic_<workload>.json (or dst)."""
+    """HBM bytes per launch of every sampler kernel from the two counter
+    runs of a --pmc-probe (PROBE_STEPS steps), their sum per step, and (for
+    the headline) k_sample_chunks alone; written to
+    profiles/traffic_<workload>.json (or dst)."""
     import csv
 
     def per_kernel(folder: str, counter: str):
@@ -289,23 +346,48 @@ def traffic_from(workload: str, fetch_dir: str, write_dir: str, dst: Path | None
                 rows[key] = rows.get(key, 0.0) + float(r["Counter_Value"])
         return rows
 
-    res = {}
+    def short(n: str) -> str:
+        n = n.split("(")[0].split("<")[0]
+        return n.split("::")[-1]
+
+    res, kernels = {}, {}
     for counter, folder in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         rows = per_kernel(folder, counter)
-        chunks = [v for (_, n), v in rows.items() if "k_sample_chunks" in n]
         copies = [v for (_, n), v in rows.items() if "copy" in n.lower() or "elementwise" in n.lower()]
-        if not chunks or not copies:
-            raise SystemExit(f"{counter}: no k_sample_chunks or copy dispatch in {folder}")
+        if not copies:
+            raise SystemExit(f"{counter}: no copy dispatch in {folder}")
         kib_copy = max(copies)
         factor = COPY_BYTES / (kib_copy * 1024.0)
-        res[counter] = {"kib_per_launch": sum(chunks) / len(chunks), "copy_kib": kib_copy,
-                        "copy_bytes": COPY_BYTES, "scale": factor,
-                        "bytes_per_launch": sum(chunks) / len(chunks) * 1024.0 * factor}
+        mine = {}
+        for (_, n), v in rows.items():
+            if short(n).startswith(("k_sample", "k_nuc", "k_verify")):
+                mine.setdefault(short(n), []).append(v)
+        if not mine:
+            raise SystemExit(f"{counter}: no sampler kernel dispatch in {folder}")
+        for name, vs in mine.items():
+            kernels.setdefault(name, {})[counter] = {
+                "launches": len(vs), "kib_per_launch": sum(vs) / len(vs),
+                "bytes_per_launch": sum(vs) / len(vs) * 1024.0 * factor}
+        res[counter] = {"copy_kib": kib_copy, "copy_bytes": COPY_BYTES, "scale": factor}
+    per_kernel_out = {}
+    step = 0.0
+    for name, c in sorted(kernels.items()):
+        b = sum(c[k]["bytes_per_launch"] for k in c)
+        per_step = b * c["FETCH_SIZE"]["launches"] / PROBE_STEPS if "FETCH_SIZE" in c else b
+        per_kernel_out[name] = {"bytes_per_launch": b, "launches_per_step": c.get("FETCH_SIZE", {}).get("launches", 0)
+                                / PROBE_STEPS, "counters": c}
+        step += per_step
     from pagellm_amd import workloads
-    w = workloads.WORKLOADS[workload]()
-    out = {"workload": workload, "kernel": "k_sample_chunks",
-           "bytes_per_launch": res["FETCH_SIZE"]["bytes_per_launch"] + res["WRITE_SIZE"]["bytes_per_launch"],
-           "algorithmic_bytes": workloads.algorithmic_bytes(w), "counters": res}
+    if workload == "spec32k":
+        alg = _spec32k_compulsory_bytes()
+    else:
+        alg = workloads.algorithmic_bytes(workloads.WORKLOADS[workload]())
+    out = {"workload": workload, "probe_steps": PROBE_STEPS, "bytes_per_step": step,
+           "algorithmic_bytes": alg, "traffic_over_algorithmic": step / alg, "per_kernel": per_kernel_out,
+           "calibration": res}
+    if "k_sample_chunks" in per_kernel_out:  # the headline's dominant kernel
+        out["kernel"] = "k_sample_chunks"
+        out["bytes_per_launch"] = per_kernel_out["k_sample_chunks"]["bytes_per_launch"]
     dst = dst if dst is not None else ROOT / "profiles" / f"traffic_{workload}.json"
     dst.write_text(json.dumps(out, indent=1) + "\n")
     print(json.dumps(out))
@@ -641,7 +723,8 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="mixed128k", choices=["mixed128k", "zipf32k", "zipf152k", "char65"])
+    ap.add_argument("--workload", default="mixed128k", choices=["mixed128k", "zipf32k", "zipf152k", "char65", "spec32k"],
+                    help="spec32k: counter probes and traffic summaries only")
     ap.add_argument("--sets", type=int, default=3, help="rotating input copies")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=256)

@@ -229,8 +229,20 @@ struct ChunkSmem {
   int ctl[8];
   uint64_t ctlu[4];
   double exp_tab[kWaves][64];  // one copy per wave
-  alignas(16) uint32_t hcnt[kHB];  // value histogram (read 16 bins per lane, 16 bytes at a time)
-  uint32_t bitmap[Geo<float>::kChunk / 32];
+  union {
+    struct {
+      alignas(16) uint32_t hcnt[kHB];  // value histogram (read 16 bins per lane, 16 bytes at a time)
+      uint32_t bitmap[Geo<float>::kChunk / 32];
+    };
+    // top-p rows: candidate buckets (kBkt of them, bucket 0 the chunk's
+    // top), used once the histogram and the penalty bitmap are done with
+    struct {
+      uint32_t bcnt[kBkt];
+      uint64_t bmass[kBkt];
+      int boff[kBkt];
+      int bcur[kBkt];
+    };
+  };
   double pz[kWaves][kPenPerWave];
   int pt[kWaves][kPenPerWave];
   // candidates staged on their way to the workspace: the raw value and
@@ -242,11 +254,6 @@ struct ChunkSmem {
   };
   uint32_t scode[kCapChunk];
   int cand_n;
-  // top-p rows: candidate buckets (kBkt of them, bucket 0 the chunk's top)
-  uint32_t bcnt[kBkt];
-  uint64_t bmass[kBkt];
-  int boff[kBkt];
-  int bcur[kBkt];
 };
 
 // Chunk-local offset of the calling lane's register slot e: the lane's
@@ -619,6 +626,14 @@ __device__ __forceinline__ void write_buckets(const SampleArgs& a, int g, double
     }
     return;
   }
+  // the buckets share their LDS with the histogram and the penalty bitmap,
+  // both done with since the barrier above
+  if (threadIdx.x < kBkt) {
+    cm.bcnt[threadIdx.x] = 0u;
+    cm.bmass[threadIdx.x] = 0ull;
+    cm.bcur[threadIdx.x] = 0;
+  }
+  wg_barrier();
   const double ymaxc = hi * invT;
   const double hbc = __builtin_floor(ymaxc * kBktPerY);
   const double* tab = cm.exp_tab[wave()];
@@ -918,11 +933,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   if (cands) {  // ordered before use by the first barrier of chunk_candidates
     for (int b = threadIdx.x; b < kHB; b += kThreads) cm.hcnt[b] = 0u;
     if (threadIdx.x == 0) cm.cand_n = 0;
-    if (!rp.topk && threadIdx.x < kBkt) {
-      cm.bcnt[threadIdx.x] = 0u;
-      cm.bmass[threadIdx.x] = 0ull;
-      cm.bcur[threadIdx.x] = 0;
-    }
   }
   int flags = 0;
   if (rp.pen_active) {

@@ -69,16 +69,35 @@ struct DrawTotal {
   double W;
 };
 
-__device__ __forceinline__ DrawTotal draw_total(const VerifyWs& ws, int b, int s, int k) {
+// The calling lane's share of row b's chunk sums (residual, p); loaded
+// before the stop position is known (they do not depend on it).
+struct PartLanes {
+  double sr, sp;
+};
+
+__device__ __forceinline__ PartLanes load_part_lanes(const VerifyWs& ws, int b) {
   const int C = ws.C;
   const double* part = ws.part + (size_t)b * C * 2;
-  double sr = 0.0, sp = 0.0;
-  for (int j = lane(); j < C; j += kWave) {
-    sr += part[2 * j];
-    sp += part[2 * j + 1];
+  // the first 64 chunks, one per lane, loaded unconditionally (lanes past
+  // C read chunk C - 1 and drop it in finish_part_lanes): no branch whose
+  // join would make the compiler wait for the loads here
+  const int j = min(lane(), C - 1);
+  return PartLanes{part[2 * j], part[2 * j + 1]};
+}
+
+__device__ __forceinline__ void finish_part_lanes(const VerifyWs& ws, int b, PartLanes& pl) {
+  const int C = ws.C;
+  const double* part = ws.part + (size_t)b * C * 2;
+  if (lane() >= C) pl = PartLanes{0.0, 0.0};
+  for (int j = lane() + kWave; j < C; j += kWave) {
+    pl.sr += part[2 * j];
+    pl.sp += part[2 * j + 1];
   }
-  sr = wave_sum(sr);
-  sp = wave_sum(sp);
+}
+
+__device__ __forceinline__ DrawTotal draw_total(const PartLanes& pl, int s, int k) {
+  const double sr = wave_sum(pl.sr);
+  const double sp = wave_sum(pl.sp);
   const bool resid = s < k && sr > 0.0;
   return DrawTotal{resid, resid ? sr : sp};
 }
@@ -154,15 +173,24 @@ __global__ __launch_bounds__(kThreads) void k_verify_draw(VerifyArgs a, VerifyWs
   __shared__ int redi[kWaves];
   const int b = blockIdx.x;
   const int k = a.k, V = a.V, C = ws.C;
-  const int s = ws.stop[b];
+  // the chunk sums and the uniforms travel with the stop position (none of
+  // their addresses depends on it); per-stop uniforms: lane i holds u_i
+  PartLanes pl = load_part_lanes(ws, b);
+  double ul = a.draw_u[a.draw_u_per_stop ? (size_t)b * (k + 1) + min(lane(), k) : (size_t)b];
+  const int s_in = ws.stop[b];
+  asm volatile("" : "+v"(ul), "+v"(pl.sr), "+v"(pl.sp));  // all of them in, before the branch on the stop
+  finish_part_lanes(ws, b, pl);
+  const int s = uniform(s_in);
   int32_t* out = a.out_tokens + (size_t)b * (k + 1);
   if (s < 0) {
     for (int i = threadIdx.x; i <= k; i += kThreads) out[i] = -1;
     if (threadIdx.x == 0) a.out_n_acc[b] = -1;
     return;
   }
-  const double u = a.draw_u_per_stop ? a.draw_u[(size_t)b * (k + 1) + s] : a.draw_u[b];
-  const DrawTotal d = draw_total(ws, b, s, k);
+  const double u = !a.draw_u_per_stop ? ul
+                   : s < kWave        ? lane_value(ul, s)
+                                      : a.draw_u[(size_t)b * (k + 1) + s];
+  const DrawTotal d = draw_total(pl, s, k);
   int tok = V - 1;  // sampling.py:98: no mass takes the last id
   if (d.W > 0.0) {
     const double t = u * d.W;
