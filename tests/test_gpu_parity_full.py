@@ -149,3 +149,14 @@ def test_unaligned_vocabulary_50257():
     assert dev.stride(0) == 50257
     ids_dev = sample_batch(dev, w["params"], uniforms=w["uniforms"], contexts=w["contexts"])
     assert np.array_equal(ids, ids_dev)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_small_batch_at_a_large_vocabulary(dtype):
+    """16 rows of the mixed batch (V = 128 256): 128 chunk workgroups (float32)
+    or 256 (float64), fewer than the chip holds at once.  Every row against
+    the oracle."""
+    w = workloads.mixed128k(rows=16)
+    w["logits"] = w["logits"].astype(dtype)
+    ids = sample_batch(w["logits"], w["params"], uniforms=w["uniforms"], contexts=w["contexts"])
+    _compare_rows(w, range(16), ids, f"mixed128k x16 {np.dtype(dtype).name}")
