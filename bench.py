@@ -394,6 +394,66 @@ def traffic_from(workload: str, fetch_dir: str, write_dir: str, dst: Path | None
     return out
 
 
+PHASES = {0: "start", 1: "wave parts", 2: "normaliser", 3: "row buckets", 4: "cut-bucket entries loaded",
+          10: "mass selection start", 11: "first level histogram", 12: "rank list", 13: "ranked",
+          5: "cut selected", 6: "per-chunk kept sums", 7: "draw bins", 8: "draw bin scattered", 9: "end"}
+
+
+def phase_stamps(steps: int = 6) -> dict:
+    """k_sample_final's phase clock stamps on mixed128k, from the profiling
+    build (python -m pagellm_amd.build --phase-stamps): per row group, the
+    median over rows and steps (the first step dropped) of the shader clock
+    ticks from the workgroup's start to each phase it reaches."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from pagellm_amd import _native, workloads
+    from pagellm_amd.sampling import _pack_histories, _pack_params
+
+    _native.LIB_PATH = ROOT / "pagellm_amd" / "_stamps" / "libpagellm_hip.so"
+    if not _native.LIB_PATH.exists():
+        raise SystemExit("build the profiling library first: python -m pagellm_amd.build --phase-stamps")
+    w = workloads.mixed128k()
+    B, V = w["logits"].shape
+    dev = torch.device("cuda:0")
+    ctx = _native.Context(0)
+    t, k, p, r = _pack_params(w["params"])
+    hist_ids, hist_off = _pack_histories(w["contexts"], w["params"], B, V)
+    x = torch.from_numpy(w["logits"]).to(dev)
+    d = {n: torch.from_numpy(a).to(dev) for n, a in
+         dict(t=t, k=k, p=p, r=r, u=w["uniforms"], ids=hist_ids, off=hist_off).items()}
+    out = torch.empty(B, dtype=torch.int32, device=dev)
+    runs = []
+    for _ in range(steps):
+        ctx.sample(x.data_ptr(), _native.PLH_F32, V, B, V, d["ids"].data_ptr(), d["off"].data_ptr(),
+                   d["t"].data_ptr(), d["k"].data_ptr(), d["p"].data_ptr(), d["r"].data_ptr(),
+                   d["u"].data_ptr(), out.data_ptr(), None, 0)
+        torch.cuda.synchronize()
+        buf = (ctypes.c_ulonglong * (256 * 16))()
+        if ctx.lib.plh_phase_stamps(buf) != 0:
+            raise SystemExit("plh_phase_stamps failed")
+        runs.append(np.frombuffer(buf, dtype=np.uint64).reshape(256, 16).astype(np.int64))
+    ctx.close()
+    a = np.stack(runs[1:])
+    res = {"workload": "mixed128k", "unit": "shader clock ticks from the workgroup's start", "groups": {}}
+    names = ["greedy", "top_k 50", "top_p 0.9", "top_k 40 + top_p 0.95 + T 0.6 + penalty 1.1"]
+    for g in range(4):
+        blk = a[:, 64 * g:64 * g + 64, :]
+        rel = blk - blk[:, :, 0:1]
+        ph = {}
+        for kk in PHASES:
+            if kk == 0:
+                continue
+            v = rel[:, :, kk].reshape(-1)
+            v = v[(v > 0) & (v < 10 ** 7)]  # phases a row does not reach keep a stale or zero stamp
+            if len(v):
+                ph[PHASES[kk]] = int(np.median(v))
+        res["groups"][f"group {g}: {names[g]}"] = dict(sorted(ph.items(), key=lambda kv: kv[1]))
+    return res
+
+
 VALU_COUNTERS = ("SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_WAVES")
 
 
@@ -732,6 +792,8 @@ def main() -> None:
     ap.add_argument("--cpu-baseline-child", action="store_true")
     ap.add_argument("--gpu-ids", help="(child) .npz of the GPU ids each configuration produced")
     ap.add_argument("--pmc-probe", action="store_true", help="short run for rocprofv3 counter passes")
+    ap.add_argument("--phase-stamps", action="store_true",
+                    help="k_sample_final's phase clock stamps on mixed128k (the profiling build)")
     ap.add_argument("--probe-group", type=int, help="(--pmc-probe) one mixed128k row group, 0-3, repeated")
     ap.add_argument("--valu-from", nargs="+", metavar="DIR",
                     help="counter run folders of --pmc-probe --probe-group 0..3 -> profiles/valu_<workload>.json")
@@ -755,6 +817,9 @@ def main() -> None:
         return
     if args.valu_kernels_from:
         valu_kernels_from(args.workload, args.valu_kernels_from)
+        return
+    if args.phase_stamps:
+        print(json.dumps(phase_stamps(), indent=1))
         return
     if args.pmc_probe:
         pmc_probe(args.workload, args.probe_group)

@@ -50,33 +50,42 @@ def _run(cmd: list[str], verbose: bool) -> None:
         sys.stderr.write(r.stdout + r.stderr)
 
 
-def build(verbose: bool = False, extra: list[str] | None = None) -> Path:
+STAMPS_DIR = PKG / "_stamps"  # the profiling build (--phase-stamps)
+
+
+def build(verbose: bool = False, extra: list[str] | None = None, phase_stamps: bool = False) -> Path:
     """Compile every HIP source and link the shared library.  Always
-    recompiles (a stale library must never hide a source change)."""
-    BUILD.mkdir(exist_ok=True)
-    extra = list(extra or [])
+    recompiles (a stale library must never hide a source change).  With
+    phase_stamps, a profiling build that records k_sample_final's phase
+    clock stamps (-DPLH_PHASE_STAMPS) goes to _stamps/ instead."""
+    build_dir = STAMPS_DIR / "_build" if phase_stamps else BUILD
+    out = STAMPS_DIR / OUT.name if phase_stamps else OUT
+    build_dir.mkdir(parents=True, exist_ok=True)
+    extra = list(extra or []) + (["-DPLH_PHASE_STAMPS"] if phase_stamps else [])
     include = ["-I", str(CSRC), "-I", str(PKG.parent / "include")]
 
     def compile_one(src: str) -> Path:
-        obj = BUILD / (Path(src).stem + ".o")
+        obj = build_dir / (Path(src).stem + ".o")
         _run([HIPCC, *FLAGS, *extra, *include, "-c", str(CSRC / src), "-o", str(obj)], verbose)
         return obj
 
     with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
         objs = list(ex.map(compile_one, SOURCES))
-    tmp = OUT.with_suffix(".so.tmp")
+    tmp = out.with_suffix(".so.tmp")
     _run([HIPCC, *FLAGS, "-shared", "-o", str(tmp), *map(str, objs)], verbose)
-    os.replace(tmp, OUT)
-    return OUT
+    os.replace(tmp, out)
+    return out
 
 
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--verbose", action="store_true")
     ap.add_argument("--resource-usage", action="store_true", help="print per-kernel register/LDS usage")
+    ap.add_argument("--phase-stamps", action="store_true",
+                    help="profiling build with k_sample_final's phase clock stamps, to pagellm_amd/_stamps/")
     args = ap.parse_args()
     extra = ["-Rpass-analysis=kernel-resource-usage"] if args.resource_usage else []
-    print(build(verbose=args.verbose or args.resource_usage, extra=extra))
+    print(build(verbose=args.verbose or args.resource_usage, extra=extra, phase_stamps=args.phase_stamps))
 
 
 if __name__ == "__main__":

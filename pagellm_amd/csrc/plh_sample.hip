@@ -38,6 +38,34 @@
 
 namespace plh {
 
+// Phase clock stamps of k_sample_final, in a profiling build only
+// (-DPLH_PHASE_STAMPS: python -m pagellm_amd.build --phase-stamps): thread
+// 0 of row r's workgroup records the shader clock on reaching phase k
+// (0 start, 1 wave parts, 2 normaliser, 3 row buckets, 4 cut-bucket entries
+// loaded, 5 cut selected, 6 per-chunk kept sums, 7 draw bins, 8 draw bin
+// scattered, 9 end; 10-13 the mass selection: start, first level's
+// histogram, rank list, ranked).  The default build compiles them out.
+#ifdef PLH_PHASE_STAMPS
+constexpr int kStampRows = 256, kStampSlots = 16;
+__device__ unsigned long long g_phase[kStampRows * kStampSlots];
+#define PLH_STAMP(row, k)                                                 \
+  do {                                                                    \
+    if (threadIdx.x == 0 && (row) < kStampRows)                           \
+      g_phase[(row) * kStampSlots + (k)] = __builtin_readcyclecounter(); \
+  } while (0)
+#define PLH_STAMP_IF(c, row, k) \
+  do {                          \
+    if (c) PLH_STAMP(row, k);   \
+  } while (0)
+#else
+#define PLH_STAMP(row, k) \
+  do {                    \
+  } while (0)
+#define PLH_STAMP_IF(c, row, k) \
+  do {                          \
+  } while (0)
+#endif
+
 constexpr int kU = 8;             // 16-byte loads per thread per chunk
 constexpr int kHB = 1024;         // histogram bins
 constexpr int kCandCap = 8192;    // candidates one row gathers
@@ -1933,6 +1961,7 @@ __device__ __forceinline__ ZSel select_z(uint32_t act, const MCands& mc, double 
   // the barrier the first level or the rank list relies on: the kernel
   // zeroes the first histogram and the rank lists at its start
   wg_barrier();
+  PLH_STAMP_IF(MASS, (int)blockIdx.x, 10);
   if (n == 0 || (!MASS && n < target)) return ZSel{false, false, 0.0, 0};
   target = uniform(target);
   uint32_t cnt = n;
@@ -1961,6 +1990,7 @@ __device__ __forceinline__ ZSel select_z(uint32_t act, const MCands& mc, double 
     }
     wg_barrier();
     const WPick pk = wave_pick2<MASS>(h, above, target);
+    PLH_STAMP_IF(MASS, (int)blockIdx.x, 11);
     if (!pk.found) return ZSel{false, false, 0.0, 0};
     above = uniform(pk.above);
     const int d = uniform(pk.d);
@@ -1977,6 +2007,7 @@ __device__ __forceinline__ ZSel select_z(uint32_t act, const MCands& mc, double 
     }
     cnt = ncnt;
   }
+  PLH_STAMP_IF(MASS, (int)blockIdx.x, 12);
   // rank list: one LDS reservation per wave
   int nq = 0;
   MC_FOR(j, mc) { nq += (act >> j) & 1u; }
@@ -2023,6 +2054,7 @@ __device__ __forceinline__ ZSel select_z(uint32_t act, const MCands& mc, double 
     lds_add(&rl.rank[ln], rank);
     if (MASS) lds_add(&rl.ahead[ln], ahead);
   }
+  PLH_STAMP_IF(MASS, (int)blockIdx.x, 13);
   wg_barrier();
   if (ln < m) {
     rank = rl.rank[ln];
@@ -2277,6 +2309,7 @@ __device__ __forceinline__ CandOut merge_topp(const SampleArgs& a, int row, cons
   const SegNorm sn = seg_norm(sg, tab, ms, &lex);
   const double invS = 1.0 / sn.S;
   const uint64_t target = topp_target(rp.top_p);
+  PLH_STAMP(row, 2);
   // the row's top bucket and this wave's chunk (INT_MIN: a chunk without
   // candidates)
   const int hbt = uniform(wave_max(bl.hb));
@@ -2311,6 +2344,7 @@ __device__ __forceinline__ CandOut merge_topp(const SampleArgs& a, int row, cons
     rv[3] = q1.y;
     rs = (rv[0] + rv[1]) + (rv[2] + rv[3]);
   }
+  PLH_STAMP(row, 3);
   const uint64_t rin = wave_scan_incl(rs, (uint64_t)0, OpAdd{});
   const uint64_t hx = __ballot(rin - rs < target && rin >= target);
   if (hx == 0ull) return CandOut{V - 1, true, sn.S};
@@ -2373,6 +2407,7 @@ __device__ __forceinline__ CandOut merge_topp(const SampleArgs& a, int row, cons
   // the cut among them, in (p desc, index asc) order (select_z orders by its
   // values, here p), starting from the mass above the bucket
   wg_barrier();
+  PLH_STAMP(row, 4);
   uint32_t nx = 0;
   for (int k = lane(); k < C; k += kWave) nx += (uint32_t)(fs.cq1[k] - fs.cq0[k]);
   nx = (uint32_t)uniform((int)wave_sum(nx));
@@ -2382,6 +2417,7 @@ __device__ __forceinline__ CandOut merge_topp(const SampleArgs& a, int row, cons
   const double plo = rstar == kBkt - 1 ? 0.0 : fast_exp_neg(yb, tab) * invS * (1.0 - 1e-9);
   const double phi = fast_exp_neg(fmin(yb + 1.0 / kBktPerY, 0.0), tab) * invS * (1.0 + 1e-9);
   const ZSel r = select_z<true>(mc.valid, mc, plo, phi, nx, target, V, fs.rl[1], fs, xw, hgen, A);
+  PLH_STAMP(row, 5);
   if (!r.found) return CandOut{V - 1, true, sn.S};
   if (ps.umax > -INFINITY) {
     // the largest token left out must fall outside the nucleus
@@ -2400,6 +2436,7 @@ __device__ __forceinline__ CandOut merge_topp(const SampleArgs& a, int row, cons
   if (threadIdx.x < G::kChunk / kDrawBins) fs.dspan[threadIdx.x] = 0ull;
   wg_barrier();
   // every wave: the chunk holding the inverse-CDF point
+  PLH_STAMP(row, 6);
   const uint64_t cs = lane() < C ? fs.csum[lane()] : 0ull;
   const uint64_t incl = wave_scan_incl(cs, (uint64_t)0, OpAdd{});
   const uint64_t tot = lane_value(incl, kWave - 1);
@@ -2437,6 +2474,7 @@ __device__ __forceinline__ CandOut merge_topp(const SampleArgs& a, int row, cons
   }
   wg_barrier();
   // every wave: the index bin, then its tokens by offset
+  PLH_STAMP(row, 7);
   const ulonglong2 b0 = reinterpret_cast<const ulonglong2*>(fs.h[0].mass)[2 * lane()];
   const ulonglong2 b1 = reinterpret_cast<const ulonglong2*>(fs.h[0].mass)[2 * lane() + 1];
   const uint64_t bv[4] = {b0.x, b0.y, b1.x, b1.y};
@@ -2461,6 +2499,7 @@ __device__ __forceinline__ CandOut merge_topp(const SampleArgs& a, int row, cons
   for (int k = 0; k < kPer; ++k)
     if (dw[k] != 0ull && (di[k] - c0) / kTokPerBin == bb) fs.dspan[di[k] - c0 - bb * kTokPerBin] = dw[k];
   wg_barrier();
+  PLH_STAMP(row, 8);
   if (wave() != 0) return CandOut{-1, false, 0.0};
   const uint64_t v = lane() < kTokPerBin ? fs.dspan[lane()] : 0ull;
   const uint64_t in3 = wave_scan_incl(v, (uint64_t)0, OpAdd{});
@@ -2474,10 +2513,11 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   __shared__ SmemAll sm;
   FastSmem& fs = sm.f;
   const int row = blockIdx.x;
-  // the first 128 candidate slots of each chunk (all a top-k row usually
-  // fills), read while the row's parameters are on their way
+  PLH_STAMP(row, 0);
   RowLoad rload;
   issue_row_params(a, row, rload);
+  // the first 128 candidate slots of each chunk (all a top-k row usually
+  // fills), read while the row's parameters are on their way
   MCands mc;
   const int sfirst = min(128, a.ws.capc);
   mc_load_first(a, row, mc, sfirst);
@@ -2517,6 +2557,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
     load_segs(a, row, (a.V + Geo<TIn>::kSeg - 1) / Geo<TIn>::kSeg, sg);
   }
   const PartSum ps = scan_parts(a, row, rp.greedy, cands, fs, pl);
+  PLH_STAMP(row, 1);
   if (cands && !bkt) mc_validate(a, row, mc, fs.wcnt[wave()], smax);
   // a chunk that could not keep all its penalised tokens aside sends the
   // row to the general pipeline
@@ -2564,6 +2605,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
     if (!general) {
       // the id is known in the lanes of the wave that drew it
       if (lane() == 0 && o.id >= 0) a.out_ids[row] = o.id;
+      PLH_STAMP(row, 9);
       return;
     }
     pin = PipeIn{true, ps.zmax, o.S > 0.0, o.S, false, 0.0};
@@ -2573,6 +2615,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
     if (threadIdx.x == 0) glb_add(a.fallback_rows, 1ull);
     id = row_general<TIn, VEC>(a, row, rp, sm.g, nullptr, pin);
   }
+  PLH_STAMP(row, 9);
   if (threadIdx.x == 0) a.out_ids[row] = id;
 }
 
@@ -3290,3 +3333,11 @@ hipError_t launch_penalize(const PenalizeArgs& a, bool f64, hipStream_t s) {
 }
 
 }  // namespace plh
+
+#ifdef PLH_PHASE_STAMPS
+// Profiling build only: copies the phase stamps of rows 0..255 (16 slots a
+// row, shader clock ticks) to host memory.
+extern "C" int plh_phase_stamps(unsigned long long* host) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(plh::g_phase), sizeof(plh::g_phase));
+}
+#endif
