@@ -48,10 +48,16 @@ def test_traffic_scaling_from_counter_runs(tmp_path):
         (3, "void plh::k_sample_chunks<float, true>(plh::SampleArgs)", 30.0),
     ])
     out = bench.traffic_from("char65", str(tmp_path / "f"), str(tmp_path / "w"), dst=tmp_path / "t.json")
-    f, w = out["counters"]["FETCH_SIZE"], out["counters"]["WRITE_SIZE"]
-    assert f["scale"] == pytest.approx(2.0) and w["scale"] == pytest.approx(1.0)
-    assert f["kib_per_launch"] == pytest.approx(2000.0) and w["kib_per_launch"] == pytest.approx(20.0)
-    assert out["bytes_per_launch"] == pytest.approx(2000.0 * 1024 * 2 + 20.0 * 1024)
+    cal = out["calibration"]
+    assert cal["FETCH_SIZE"]["scale"] == pytest.approx(2.0) and cal["WRITE_SIZE"]["scale"] == pytest.approx(1.0)
+    ch = out["per_kernel"]["k_sample_chunks"]["counters"]
+    assert ch["FETCH_SIZE"]["kib_per_launch"] == pytest.approx(2000.0)
+    assert ch["WRITE_SIZE"]["kib_per_launch"] == pytest.approx(20.0)
+    chunks = 2000.0 * 1024 * 2 + 20.0 * 1024
+    assert out["bytes_per_launch"] == pytest.approx(chunks)  # the headline kernel alone
+    final = 99999.0 * 1024 * 2  # one launch in the probe's PROBE_STEPS steps
+    # per step: each kernel's bytes per launch times its launches per step
+    assert out["bytes_per_step"] == pytest.approx((2 * chunks + final) / bench.PROBE_STEPS)
     assert (tmp_path / "t.json").exists()
 
 
