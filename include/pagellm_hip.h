@@ -106,7 +106,9 @@ int plh_sync(plh_ctx* ctx);
  * src/pagellm/engine/sampling.py:101-107 (sample), :65-91 (probs),
  * :94-98 (draw), :52-62 (apply_repetition_penalty).
  *
- *   logits      [B, ld] of `dtype` (PLH_F32 / PLH_F64); row b starts at b*ld
+ *   logits      [B, ld] of `dtype` (PLH_F32 / PLH_F64); row b starts at b*ld;
+ *               aligned to its element size (rows of any 16-byte alignment
+ *               take the same kernels)
  *   hist_ids    int32 token ids, CSR over rows (the sequence's full history,
  *               prompt + outputs, llm_engine.py:283); may be NULL with
  *   hist_off    int64 [B+1] offsets into hist_ids, or NULL (no history);
@@ -139,8 +141,12 @@ int plh_sample(plh_ctx* ctx, const void* logits, int dtype, int64_t ld, int B, i
  * context is created), never the context's growable workspace, and the
  * kernel-timing option is ignored.  A batch whose workspace exceeds 64 MiB
  * returns PLH_ERR_INVALID_ARG (mixed128k, 256 x 128256 fp32, fits).  Every
- * call on one GPU shares that GPU's array: calls that overlap on one GPU
- * (two streams, two contexts) race.
+ * call on one GPU shares that GPU's array.  Calls of one context are
+ * ordered on it: when the context's stream changed since its last call,
+ * the new stream first waits on an event that call recorded (created by
+ * plh_create); under graph capture such a stream change returns
+ * PLH_ERR_INVALID_ARG.  Calls of different contexts that overlap on one GPU
+ * race.
  */
 int plh_sample_noalloc(plh_ctx* ctx, const void* logits, int dtype, int64_t ld, int B, int V,
                        const int32_t* hist_ids, const int64_t* hist_off, const double* temperature,
@@ -150,9 +156,10 @@ int plh_sample_noalloc(plh_ctx* ctx, const void* logits, int dtype, int64_t ld, 
 /*
  * apply_repetition_penalty() on a copy: src/pagellm/engine/sampling.py:52-62.
  * out[b, :V] = x[b, :V] with every distinct id of row b's history mapped
- * through x > 0 ? x / penalty : x * penalty, computed in `dtype`.  `out`
- * must not overlap `x` (PLH_ERR_INVALID_ARG): the penalty works on a copy,
- * as the reference's does (:58).
+ * through x > 0 ? x / penalty : x * penalty, computed in `dtype`.  No row
+ * of `out` may overlap a row of `x` (PLH_ERR_INVALID_ARG): the penalty works
+ * on a copy, as the reference's does (:58).  Interleaved rows of one buffer
+ * (x = buf[:, :V], out = buf[:, V:2V], the same ld) are allowed.
  */
 int plh_penalize(plh_ctx* ctx, const void* x, int dtype, int64_t ld, int B, int V,
                  const int32_t* hist_ids, const int64_t* hist_off, const double* rep_penalty,
