@@ -22,12 +22,14 @@ struct WavePart {
 constexpr int kChunkIncomplete = 1;
 
 // Per-row state of the nucleus path (rows with no top-k and a top_p of at
-// least kNucTopP, when the caller asks for it): three passes over the row
-// (segment partials, a count histogram of y = z / T, the tokens of the
-// bins that can hold the cut) instead of the general pipeline.
+// least kNucTopP, when the caller asks for it): two passes over the row
+// (segment partials and per-chunk count histograms of z, then the tokens of
+// the bins that can hold the cut) instead of the general pipeline.  The
+// row's bins lie on a power-of-two grid: bin b holds the tokens whose z,
+// rounded to float, has floor(zf * rz) = base + b (zf * rz is exact).
 struct NucRow {
-  double zlo;    // lower edge of the count histogram: the smallest finite penalised logit
-  double scale;  // bins per unit of z
+  float rz;      // bins per unit of z, a power of two
+  int base;      // floor(zf * rz) of the row's smallest finite penalised logit
   double ymax;   // largest y = z / T of the row
   double S;      // sum over the row of exp(y - ymax)
   double invS;
@@ -37,6 +39,13 @@ struct NucRow {
   int above;     // 1: nexcl sums the tokens above the window (fewer than those below)
 };
 constexpr int kNucActive = 1;
+// A chunk's own histogram grid: bin j holds floor(zf * rz) = q0 + j; rz is
+// the largest power of two that fits the chunk's span in kNucBins bins (0:
+// the chunk holds no finite token).
+struct NucGrid {
+  float rz;
+  int q0;
+};
 constexpr int kNucPenWords = 512;  // bitmap words of one chunk (16384 float tokens)
 constexpr int kNucBins = 2048;
 constexpr int kBkt = 256;          // candidate buckets of a top-p chunk
@@ -50,7 +59,9 @@ struct ChunkWs {
   double* cz;       // [B * C * capc] candidate penalised logits
   int32_t* ci;      // [B * C * capc] candidate token ids
   NucRow* nrow;     // [B] nucleus path: per-row state
-  uint32_t* ncnt;   // [B * kNucBins] nucleus path: token counts per y bin
+  uint32_t* nhist;  // [B * C * kNucBins / 2] nucleus path: each chunk's token counts per bin of its own
+                    // grid, two 16-bit counts a word
+  NucGrid* ngrid;   // [B * C] nucleus path: each chunk's grid (NucGrid)
   double* nexcl;    // [B * C * 8] nucleus path: per-segment mass on one side of the candidate bins
   int32_t* ncand;   // [B * C] nucleus path: candidates per chunk (-1: over capacity)
   uint32_t* npen;   // [B * C * kNucPenWords] nucleus path: each chunk's penalised-token bitmap

@@ -927,6 +927,36 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
 // the blocks of one row all carry the same b % 8, so a row's chunks and its
 // merge (block `row` of the per-row grids) share one XCD's L2.  -1: a
 // padding block (B not a multiple of 8).
+// Nucleus bins lie on power-of-two grids: with rz = 2^e bins per unit of z,
+// a token's bin is floor(zf * rz) for zf its z rounded to float (zf * rz is
+// exact, so the bins are exact half-open intervals of zf, monotone in z).
+// A grid of 2^e nests inside every finer one: floor(zf * 2^(e + s)) >> s =
+// floor(zf * 2^e).  nuc_fit returns the largest rz (2^-40 .. 2^24) that
+// fits [lo, hi] in kNucBins bins with every floor(zf * rz) within +-2^30;
+// rz = 0 when there is no finite value, -1 when the values are too large
+// to bin (|z| >= 2^70).
+__device__ __forceinline__ NucGrid nuc_fit(float lo, float hi) {
+  if (!(hi >= lo)) return NucGrid{0.0f, 0};  // no finite value (hi = -inf, lo = +inf)
+  const float mag = fmaxf(fabsf(lo), fabsf(hi));
+  if (!(mag < 1.1805916e21f)) return NucGrid{-1.0f, 0};  // 2^70
+  int e = 24;
+  if (hi > lo) {
+    const float r = (float)(kNucBins - 2) / (hi - lo);
+    e = r >= 16777216.0f ? 24 : (r < 9.094947e-13f ? -40 : min(24, (int)floorf(log2f(r))));  // 2^24, 2^-40
+  }
+  if (mag > 0.0f) e = min(e, 29 - (int)ceilf(log2f(mag)));
+  e = max(e, -40);
+  float rz = ldexpf(1.0f, e);
+  while (e > -40 && __float2int_rd(hi * rz) - __float2int_rd(lo * rz) > kNucBins - 1) {
+    rz *= 0.5f;
+    --e;
+  }
+  return NucGrid{rz, __float2int_rd(lo * rz)};
+}
+
+// The exponent of a power-of-two float.
+__device__ __forceinline__ int pow2_exp(float rz) { return ((__float_as_int(rz) >> 23) & 0xff) - 127; }
+
 constexpr int kXcds = 8;
 __device__ __forceinline__ int chunk_block(int C, int B) {
   const int x = (int)blockIdx.x % kXcds, k = (int)blockIdx.x / kXcds;
@@ -1020,9 +1050,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   if (cands) chunk_candidates<TIn>(tk, lmax, wmax, m2, by_max, target, fl, !rp.topk && C <= kWaves, 1.0 / rp.T, a, g, c0,
                                      flags, wp, cm);
   else if (lane() == 0) wp->flags = flags;
-  if (NUC && rp.nucleus && g == row * C)  // the row's count histogram, filled by k_nuc_hist
-    for (int b = threadIdx.x; b < kNucBins; b += kThreads) a.ws.ncnt[(size_t)row * kNucBins + b] = 0u;
-  if (NUC && rp.nucleus) {  // the range of the row's count histogram
+  if (NUC && rp.nucleus) {  // the row's range, and this chunk's count histogram
     // the smallest finite register token (-inf slots count as +inf)
     const TIn inf = (TIn)INFINITY;
     TIn lmn = inf;
@@ -1042,6 +1070,43 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       wp->umax = zmn;  // the nucleus kernels' lower range edge
       wp->zmax = wmax;
     }
+    // the chunk's tokens counted on its own power-of-two grid, in the
+    // candidate staging area (nucleus rows stage no candidates); k_nuc_window
+    // merges the chunks' histograms on the row's grid
+    uint32_t* nh = reinterpret_cast<uint32_t*>(cm.sraw);
+    static_assert(sizeof(cm.sraw) >= kNucBins * sizeof(uint32_t), "the staging area holds the histogram");
+    for (int b = threadIdx.x; b < kNucBins; b += kThreads) nh[b] = 0u;
+    if (lane() == 0) {
+      cm.redd[wave()] = zmn;
+      cm.redd[kWaves + wave()] = wmax;
+    }
+    wg_barrier();
+    double clo = cm.redd[0], chi = cm.redd[kWaves];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+      clo = fmin(clo, cm.redd[w]);
+      chi = fmax(chi, cm.redd[kWaves + w]);
+    }
+    const NucGrid grid = nuc_fit((float)clo, (float)chi);
+    if (grid.rz > 0.0f) {
+      uint32_t one = 1u;  // kept in a register, not rematerialised for every slot
+      asm volatile("" : "+v"(one));
+      tk.new_pass();
+#pragma unroll
+      for (int e = 0; e < G::kEpt; ++e) {
+        const TIn v = tk.rv(e);
+        if (v > (TIn)(-INFINITY)) lds_add(&nh[__float2int_rd((float)v * grid.rz) - grid.q0], one);
+      }
+      for (int i = 0; i < tk.np; ++i) {
+        const double z = tk.pen_z(cm, i);
+        if (z > -INFINITY) lds_add(&nh[__float2int_rd((float)z * grid.rz) - grid.q0], 1u);
+      }
+    }
+    wg_barrier();
+    // two 16-bit counts a word (a chunk holds at most 16384 tokens)
+    uint32_t* out = a.ws.nhist + (size_t)g * (kNucBins / 2);
+    for (int w = threadIdx.x; w < kNucBins / 2; w += kThreads) out[w] = nh[2 * w] | (nh[2 * w + 1] << 16);
+    if (threadIdx.x == 0) a.ws.ngrid[g] = grid;
   }
   if (!rp.topk) {  // the full-vocabulary normaliser (sampling.py:79-81)
     // y = z / T is monotone in z, so the segment's max y is y(max z)
@@ -2568,24 +2633,36 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
     if (general) {
       if (threadIdx.x == 0) a.ws.nrow[row].state = 0;  // finished here: the nucleus kernels skip it
     } else {
-      // the nucleus kernels finish the row; its count histogram spans the
-      // row's finite penalised logits
+      // the nucleus kernels finish the row; its bins span the row's finite
+      // penalised logits on a power-of-two grid no finer than any chunk's
       if (wave() == 0) {
-        const WavePart* pp = a.ws.part + (size_t)row * a.ws.C * kWaves;
+        const int C = a.ws.C;
+        const WavePart* pp = a.ws.part + (size_t)row * C * kWaves;
         double lo = INFINITY, hi = -INFINITY;
-        for (int j = lane(); j < a.ws.C * kWaves; j += kWave) {
+        for (int j = lane(); j < C * kWaves; j += kWave) {
           lo = fmin(lo, pp[j].umax);  // nucleus rows: the wave's smallest finite logit
           hi = fmax(hi, pp[j].zmax);
         }
+        float crz = INFINITY;
+        int bad = 0;
+        for (int j = lane(); j < C; j += kWave) {
+          const float r = a.ws.ngrid[(size_t)row * C + j].rz;
+          if (r < 0.0f) bad = 1;
+          if (r > 0.0f) crz = fminf(crz, r);
+        }
         lo = wave_min(lo);
         hi = wave_max(hi);
+        crz = wave_min(crz);
+        bad = wave_max(bad);
         if (lane() == 0) {
-          const double scale = (double)kNucBins / (hi - lo);
+          const NucGrid rg = nuc_fit((float)lo, (float)hi);
+          const float rz = fminf(rg.rz, crz);
           NucRow& nr = a.ws.nrow[row];
-          nr.zlo = lo;
-          nr.scale = scale;
-          // one distinct finite value, or none: the general pipeline (k_nuc_final)
-          nr.general = (hi - lo > 0.0 && hi - lo < INFINITY && scale < INFINITY) ? 0 : 1;
+          nr.rz = rz;
+          nr.base = rz > 0.0f ? __float2int_rd((float)lo * rz) : 0;
+          // one distinct finite value, or none, or logits too large to bin:
+          // the general pipeline (k_nuc_final)
+          nr.general = (hi - lo > 0.0 && hi - lo < INFINITY && rg.rz > 0.0f && !bad) ? 0 : 1;
           nr.state = kNucActive;
         }
       }
@@ -2625,12 +2702,13 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
 // any candidate list holds.  With the caller's hint they take passes over
 // all chunks instead of one workgroup per row: k_sample_chunks leaves the
 // segment partials of the normaliser, each wave's smallest and largest
-// finite logit and (penalised rows) each chunk's bitmap of penalised
-// tokens, and zeroes the row's counts; k_sample_final spreads kNucBins
-// affine bins over the row's range of z (or finishes the row itself when a
-// chunk could not set its penalised tokens aside); then
-//   k_nuc_hist    counts the row's tokens per bin;
-//   k_nuc_window  bounds each bin's mass by its count and the exp of its
+// finite logit, (penalised rows) each chunk's bitmap of penalised tokens,
+// and each chunk's count histogram on a power-of-two grid of its own (the
+// finest that fits the chunk's range in kNucBins bins); k_sample_final
+// picks the row's grid, no finer than any chunk's (or finishes the row
+// itself when a chunk could not set its penalised tokens aside); then
+//   k_nuc_window  adds the chunks' histograms into the row's bins and
+//                 bounds each bin's mass by its count and the exp of its
 //                 edges, which brackets the top-p cut (sampling.py:82-90) in a
 //                 window of bins: the bins below it hold at most 1 - top_p
 //                 of the mass (dropped), those above it more than that below
@@ -2644,22 +2722,24 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
 // A row whose window does not fit its candidate slots, or whose cut falls
 // outside the window, is finished by the general pipeline.
 
-// Bin of a nucleus row's token: floor((z - zlo) * scale) clamped to
-// [0, kNucBins - 1], computed in float32 on z rounded to float.  Monotone
-// non-decreasing in z; every kernel that bins a token uses this function.
+// Bin of a nucleus row's token on the row's grid (NucRow rz, base), clamped
+// to [0, kNucBins - 1].  Every kernel that bins a token uses this function.
 struct NucBin {
-  float lo, scale, top;
-  __device__ __forceinline__ explicit NucBin(const NucRow& nr) : lo((float)nr.zlo), scale((float)nr.scale) {
-    // the clamp's upper end lives in a register: v_med3_f32 takes no
+  float rz;
+  int base, top;
+  __device__ __forceinline__ explicit NucBin(const NucRow& nr) : rz(nr.rz), base(nr.base) {
+    // the clamp's upper end lives in a register: v_med3_i32 takes no
     // literal, and the compiler would otherwise rebuild it for every token
-    top = (float)(kNucBins - 1);
+    top = kNucBins - 1;
     asm volatile("" : "+v"(top));
   }
   __device__ __forceinline__ int operator()(float zf) const {
-    const float t = (zf - lo) * scale;
-    return (int)__builtin_amdgcn_fmed3f(t, 0.0f, top);
+    return min(max(__float2int_rd(zf * rz) - base, 0), top);
   }
   __device__ __forceinline__ int operator()(double z) const { return (*this)((float)z); }
+  // bin 0's lower edge in z and the bins per unit of z
+  __device__ __forceinline__ double lo() const { return (double)base / (double)rz; }
+  __device__ __forceinline__ double scale() const { return (double)rz; }
 };
 
 // The calling lane's penalty bits (as chunk_pbits) from the chunk bitmap
@@ -2683,52 +2763,8 @@ __device__ __forceinline__ double nuc_p(double y, const NucRow& nr, const double
   return fast_exp_neg(y - nr.ymax, tab) * nr.invS;
 }
 
-template <typename TIn, bool VEC>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_nuc_hist(SampleArgs a) {
-  using G = Geo<TIn>;
-  __shared__ ChunkSmem cm;
-  __shared__ uint32_t nh[kNucBins];
-  const int C = a.ws.C;
-  const int g = chunk_block(C, a.B);
-  if (g < 0) return;
-  const int row = g / C;
-  const RowParams rp = load_row_params(a, row);
-  if (!rp.nucleus) return;
-  const int c0 = (g - row * C) * G::kChunk;
-  const TIn* x = reinterpret_cast<const TIn*>(a.logits) + (int64_t)row * a.ld;
-  ChunkToks<TIn> tk;
-  load_chunk<TIn, VEC>(x, a.V, c0, tk.v);  // in flight while the row's state is read
-  const NucRow nr = a.ws.nrow[row];
-  if (nr.state != kNucActive || nr.general != 0) return;
-  for (int b = threadIdx.x; b < kNucBins; b += kThreads) nh[b] = 0u;
-  if (rp.pen_active) {
-    // the first pass set aside the same tokens without overflow, or the
-    // row would not be here
-    set_aside_penalised<TIn>(tk, nuc_pbits<TIn>(a, g), rp.pen, c0, cm);
-  }
-  wg_barrier();
-  const NucBin nb(nr);
-  uint32_t one = 1u;  // kept in a register, not rematerialised for every slot
-  asm volatile("" : "+v"(one));
-  tk.new_pass();
-#pragma unroll
-  for (int e = 0; e < G::kEpt; ++e) {
-    const TIn v = tk.rv(e);
-    if (v > (TIn)(-INFINITY)) lds_add(&nh[nb((float)v)], one);
-  }
-  for (int i = 0; i < tk.np; ++i) {
-    const double z = tk.pen_z(cm, i);
-    if (z > -INFINITY) lds_add(&nh[nb(z)], 1u);
-  }
-  wg_barrier();
-  uint32_t* cnt = a.ws.ncnt + (size_t)row * kNucBins;
-  for (int b = threadIdx.x; b < kNucBins; b += kThreads) {
-    const uint32_t n = nh[b];
-    if (n != 0u) atomicAdd(&cnt[b], n);
-  }
-}
-
 struct NucWinSmem {
+  uint32_t rowh[kNucBins];  // the row's counts on its grid
   double exp_tab[kWaves][64];
   double redd[2 * kWaves];
   int redi[2 * kWaves];
@@ -2757,20 +2793,53 @@ __global__ __launch_bounds__(kThreads) void k_nuc_window(SampleArgs a) {
   const double* tab = sm.exp_tab[wave()];
   constexpr int kPer = kNucBins / kThreads;
   const int b0 = kPer * (int)threadIdx.x;
-  uint32_t c[kPer];
-  const uint32_t* gcnt = a.ws.ncnt + (size_t)row * kNucBins;
+  // the row's counts: each chunk's histogram (its own grid, nested in the
+  // row's: shift by the exponent difference) added into the row's bins
+  for (int b = threadIdx.x; b < kNucBins; b += kThreads) sm.rowh[b] = 0u;
+  {
+    const int C = a.ws.C;
+    const int erow = pow2_exp(nr.rz);
+    const NucGrid* grids = a.ws.ngrid + (size_t)row * C;
+    const uint32_t* hist = a.ws.nhist + (size_t)row * C * (kNucBins / 2);
+    wg_barrier();
+    constexpr int kWordsPerThread = kNucBins / 2 / kThreads;  // 2
+    constexpr int kBatch = 8;                                 // chunks whose words are loaded at once
+    for (int c0 = 0; c0 < C; c0 += kBatch) {
+      uint32_t wv[kBatch][kWordsPerThread];
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) c[j] = gcnt[b0 + j];
+      for (int k = 0; k < kBatch; ++k)
+#pragma unroll
+        for (int w = 0; w < kWordsPerThread; ++w)
+          wv[k][w] = c0 + k < C ? hist[(size_t)(c0 + k) * (kNucBins / 2) + threadIdx.x + w * kThreads] : 0u;
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        if (c0 + k >= C) break;
+        const NucGrid gq = grids[c0 + k];
+        if (!(gq.rz > 0.0f)) continue;
+        const int sh = pow2_exp(gq.rz) - erow;  // >= 0: the row's grid is no finer
+#pragma unroll
+        for (int w = 0; w < kWordsPerThread; ++w) {
+          const int j = 2 * ((int)threadIdx.x + w * kThreads);
+          const uint32_t v = wv[k][w];
+          if (v & 0xffffu) lds_add(&sm.rowh[min(max(((gq.q0 + j) >> sh) - nr.base, 0), kNucBins - 1)], v & 0xffffu);
+          if (v >> 16) lds_add(&sm.rowh[min(max(((gq.q0 + j + 1) >> sh) - nr.base, 0), kNucBins - 1)], v >> 16);
+        }
+      }
+    }
+    wg_barrier();
+  }
+  uint32_t c[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) c[j] = sm.rowh[b0 + j];
   SegLoad sg;
   load_segs(a, row, (a.V + G::kSeg - 1) / G::kSeg, sg);
   double ms[kSegPerLane], lex;
   const SegNorm sn = seg_norm(sg, tab, ms, &lex);
   const double invT = 1.0 / rp.T;
-  // NucBin works in float32: its edges are those of the rounded lo and
-  // scale, and rounding z to float moves a token by up to 2^-24 |z|, which
-  // the margin covers with room to spare
+  // NucBin bins z rounded to float on an exact grid: rounding z moves a
+  // token by up to 2^-24 |z|, which the margin covers with room to spare
   const NucBin nbin(nr);
-  const double flo = (double)nbin.lo, fsc = (double)nbin.scale;
+  const double flo = nbin.lo(), fsc = nbin.scale();
   const double mag = fmax(fabs(flo), fabs(flo + (double)kNucBins / fsc));
   const double mb = 0.01 + mag * fsc * 2.5e-7;
   double lo[kPer], hi[kPer], slo = 0.0, shi = 0.0;
@@ -3226,7 +3295,7 @@ size_t fast_ws_bytes(int B, int V, bool f64) {
   const size_t C = (size_t)chunks_of(V, f64), cap = (size_t)capc_of((int)C), n = (size_t)B * C;
   return up256(n * kWaves * sizeof(WavePart)) + 2 * up256(n * kWaves * sizeof(double)) + up256(n * cap * sizeof(double)) +
          up256(n * cap * sizeof(int32_t)) + up256((size_t)B * sizeof(NucRow)) +
-         up256((size_t)B * kNucBins * sizeof(uint32_t)) + up256(n * kWaves * sizeof(double)) + up256(n * sizeof(int32_t)) +
+         up256(n * (kNucBins / 2) * sizeof(uint32_t)) + up256(n * sizeof(NucGrid)) + up256(n * kWaves * sizeof(double)) + up256(n * sizeof(int32_t)) +
          up256(n * kNucPenWords * sizeof(uint32_t)) + up256(n * kBkt * sizeof(uint64_t)) +
          up256(n * kBkt * sizeof(uint32_t)) + up256(n * sizeof(double)) + up256(n * sizeof(int32_t));
 }
@@ -3249,8 +3318,10 @@ ChunkWs fast_ws_layout(void* base, int B, int V, bool f64) {
   p += up256(n * w.capc * sizeof(int32_t));
   w.nrow = reinterpret_cast<NucRow*>(p);
   p += up256((size_t)B * sizeof(NucRow));
-  w.ncnt = reinterpret_cast<uint32_t*>(p);
-  p += up256((size_t)B * kNucBins * sizeof(uint32_t));
+  w.nhist = reinterpret_cast<uint32_t*>(p);
+  p += up256(n * (kNucBins / 2) * sizeof(uint32_t));
+  w.ngrid = reinterpret_cast<NucGrid*>(p);
+  p += up256(n * sizeof(NucGrid));
   w.nexcl = reinterpret_cast<double*>(p);
   p += up256(n * kWaves * sizeof(double));
   w.ncand = reinterpret_cast<int32_t*>(p);
@@ -3301,13 +3372,10 @@ hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, int num_c
   }
   hipLaunchKernelGGL(finals[f64][vec][nuc], gf, block, 0, s, a);
   if (a.nucleus) {
-    auto hist = f64 ? (vec ? k_nuc_hist<double, true> : k_nuc_hist<double, false>)
-                    : (vec ? k_nuc_hist<float, true> : k_nuc_hist<float, false>);
     auto cands = f64 ? (vec ? k_nuc_cands<double, true> : k_nuc_cands<double, false>)
                      : (vec ? k_nuc_cands<float, true> : k_nuc_cands<float, false>);
     auto fin = f64 ? (vec ? k_nuc_final<double, true> : k_nuc_final<double, false>)
                    : (vec ? k_nuc_final<float, true> : k_nuc_final<float, false>);
-    hipLaunchKernelGGL(hist, dim3(total), block, 0, s, a);
     hipLaunchKernelGGL(f64 ? k_nuc_window<double> : k_nuc_window<float>, gf, block, 0, s, a);
     hipLaunchKernelGGL(cands, dim3(total), block, 0, s, a);
     hipLaunchKernelGGL(fin, gf, block, 0, s, a);
