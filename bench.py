@@ -399,11 +399,57 @@ PHASES = {0: "start", 1: "wave parts", 2: "normaliser", 3: "row buckets", 4: "cu
           5: "cut selected", 6: "per-chunk kept sums", 7: "draw bins", 8: "draw bin scattered", 9: "end"}
 
 
+CHUNK_PHASES = {1: "register maxima", 2: "chunk range", 3: "threshold", 4: "counted", 5: "placed",
+                6: "buckets written", 7: "end (wave 0)"}
+
+
+def chunk_timeline(ph, rt, hw, B: int, C: int) -> dict:
+    """k_sample_chunks' stamps of one step (ph [g, 8] shader clock, rt [g, 9]
+    real-time clock: start, then each wave's end, hw [g, 2] HW_ID and XCC_ID):
+    the clock rate, the kernel's span, the workgroups' lifetimes, how many
+    were resident per CU on average and over time, and the gap between a
+    workgroup's last wave ending and the next workgroup starting in the CU
+    slot it freed."""
+    import numpy as np
+
+    n = B * C
+    ph, rt, hw = ph[:n], rt[:n], hw[:n]
+    start, wend = rt[:, 0], rt[:, 1:]
+    end = wend.max(axis=1)
+    life = end - start
+    ghz = float(np.median((ph[:, 7] - ph[:, 0]) / np.maximum(wend[:, 0] - start, 1))) / 10.0
+    cu = ((hw[:, 1] & 0xF) * 8 + ((hw[:, 0] >> 13) & 7)) * 32 + ((hw[:, 0] >> 12) & 1) * 16 + ((hw[:, 0] >> 8) & 0xF)
+    t0, span = start.min(), end.max() - start.min()
+    cus = np.unique(cu)
+    bins = 10
+    edges = t0 + span * (np.arange(bins) + 0.5) / bins
+    occ = [float(((start[None, :] <= e) & (end[None, :] > e)).sum()) / len(cus) for e in edges]
+    gaps = []
+    for c in cus:
+        idx = np.where(cu == c)[0]
+        idx = idx[np.argsort(start[idx])]
+        held = []
+        for j in idx:
+            held.sort()
+            if len(held) >= 2:
+                gaps.append(start[j] - held.pop(0))
+            held.append(end[j])
+    us = 0.01  # real-time clock: 100 MHz
+    return {"clock_ghz": round(ghz, 3), "cus": int(len(cus)), "span_us": round(float(span) * us, 2),
+            "workgroup_life_us_median": round(float(np.median(life)) * us, 2),
+            "resident_workgroups_per_cu_mean": round(float(life.sum()) / (len(cus) * float(span)), 2),
+            "resident_workgroups_per_cu_over_time": [round(v, 2) for v in occ],
+            "slot_refill_gap_us_median": round(float(np.median(gaps)) * us, 3) if gaps else None,
+            "wave0_end_to_last_wave_end_us_median": round(float(np.median(end - wend[:, 0])) * us, 3)}
+
+
 def phase_stamps(steps: int = 6) -> dict:
-    """k_sample_final's phase clock stamps on mixed128k, from the profiling
-    build (python -m pagellm_amd.build --phase-stamps): per row group, the
-    median over rows and steps (the first step dropped) of the shader clock
-    ticks from the workgroup's start to each phase it reaches."""
+    """k_sample_final's and k_sample_chunks' phase clock stamps on
+    mixed128k, from the profiling build (python -m pagellm_amd.build
+    --phase-stamps): per row group, the median over rows (chunks) and steps
+    (the first step dropped) of the shader clock ticks from the workgroup's
+    start to each phase it reaches; for the chunk kernel also its timeline
+    (chunk_timeline) per step."""
     import ctypes
 
     import numpy as np
@@ -425,7 +471,8 @@ def phase_stamps(steps: int = 6) -> dict:
     d = {n: torch.from_numpy(a).to(dev) for n, a in
          dict(t=t, k=k, p=p, r=r, u=w["uniforms"], ids=hist_ids, off=hist_off).items()}
     out = torch.empty(B, dtype=torch.int32, device=dev)
-    runs = []
+    runs, cruns = [], []
+    C = (V + 16383) // 16384  # 64 KB chunks of float32
     for _ in range(steps):
         ctx.sample(x.data_ptr(), _native.PLH_F32, V, B, V, d["ids"].data_ptr(), d["off"].data_ptr(),
                    d["t"].data_ptr(), d["k"].data_ptr(), d["p"].data_ptr(), d["r"].data_ptr(),
@@ -435,9 +482,27 @@ def phase_stamps(steps: int = 6) -> dict:
         if ctx.lib.plh_phase_stamps(buf) != 0:
             raise SystemExit("plh_phase_stamps failed")
         runs.append(np.frombuffer(buf, dtype=np.uint64).reshape(256, 16).astype(np.int64))
+        cph, crt, chw = (ctypes.c_ulonglong * (4096 * 8))(), (ctypes.c_ulonglong * (4096 * 9))(), (ctypes.c_uint * (4096 * 2))()
+        if ctx.lib.plh_chunk_stamps(cph, crt, chw) != 0:
+            raise SystemExit("plh_chunk_stamps failed")
+        cruns.append((np.frombuffer(cph, dtype=np.uint64).reshape(4096, 8).astype(np.int64),
+                      np.frombuffer(crt, dtype=np.uint64).reshape(4096, 9).astype(np.int64),
+                      np.frombuffer(chw, dtype=np.uint32).reshape(4096, 2).astype(np.int64)))
     ctx.close()
     a = np.stack(runs[1:])
-    res = {"workload": "mixed128k", "unit": "shader clock ticks from the workgroup's start", "groups": {}}
+    res = {"workload": "mixed128k", "unit": "shader clock ticks from the workgroup's start", "groups": {},
+           "chunk_groups": {}, "chunk_timeline": [chunk_timeline(*r, B, C) for r in cruns[1:]]}
+    cph = np.stack([r[0][:B * C] for r in cruns[1:]])
+    for g in range(4):
+        blk = cph[:, 64 * g * C:64 * (g + 1) * C, :]
+        rel = blk - blk[:, :, 0:1]
+        ph = {}
+        for kk, name in CHUNK_PHASES.items():
+            v = rel[:, :, kk].reshape(-1)
+            v = v[(v > 0) & (v < 10 ** 7)]
+            if len(v):
+                ph[name] = int(np.median(v))
+        res["chunk_groups"][f"group {g}"] = ph
     names = ["greedy", "top_k 50", "top_p 0.9", "top_k 40 + top_p 0.95 + T 0.6 + penalty 1.1"]
     for g in range(4):
         blk = a[:, 64 * g:64 * g + 64, :]

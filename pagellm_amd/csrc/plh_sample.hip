@@ -38,7 +38,7 @@
 
 namespace plh {
 
-// Phase clock stamps of k_sample_final, in a profiling build only
+// Phase clock stamps of k_sample_final and k_sample_chunks, in a profiling build only
 // (-DPLH_PHASE_STAMPS: python -m pagellm_amd.build --phase-stamps): thread
 // 0 of row r's workgroup records the shader clock on reaching phase k
 // (0 start, 1 wave parts, 2 normaliser, 3 row buckets, 4 cut-bucket entries
@@ -57,12 +57,43 @@ __device__ unsigned long long g_phase[kStampRows * kStampSlots];
   do {                          \
     if (c) PLH_STAMP(row, k);   \
   } while (0)
+// k_sample_chunks, per chunk g < kStampChunks: thread 0 records the shader
+// clock on reaching phase k (0 start, 1 register maxima, 2 chunk range, 3
+// threshold, 4 counted, 5 placed, 6 buckets written, 7 end), the real-time
+// clock (100 MHz, one count for the whole GPU) at its start, and the
+// workgroup's hardware id and XCD; lane 0 of each wave records the
+// real-time clock at the wave's end.
+constexpr int kStampChunks = 4096, kChunkSlots = 8;
+__device__ unsigned long long g_cphase[kStampChunks * kChunkSlots];
+__device__ unsigned long long g_crt[kStampChunks * (1 + kWaves)];
+__device__ unsigned int g_chw[kStampChunks * 2];
+#define PLH_CSTAMP(g, k)                                                        \
+  do {                                                                          \
+    if (threadIdx.x == 0 && (g) < kStampChunks) {                               \
+      g_cphase[(g) * kChunkSlots + (k)] = __builtin_readcyclecounter();         \
+      if ((k) == 0) {                                                           \
+        g_crt[(g) * (1 + kWaves)] = __builtin_amdgcn_s_memrealtime();           \
+        g_chw[(g) * 2] = __builtin_amdgcn_s_getreg((31 << 11) | 4);  /* HW_ID */ \
+        g_chw[(g) * 2 + 1] = __builtin_amdgcn_s_getreg((31 << 11) | 20); /* XCC_ID */ \
+      }                                                                         \
+    }                                                                           \
+  } while (0)
+#define PLH_CWAVE_END(g)                                                                          \
+  do {                                                                                            \
+    if (lane() == 0 && (g) < kStampChunks) g_crt[(g) * (1 + kWaves) + 1 + wave()] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
 #else
 #define PLH_STAMP(row, k) \
   do {                    \
   } while (0)
 #define PLH_STAMP_IF(c, row, k) \
   do {                          \
+  } while (0)
+#define PLH_CSTAMP(g, k) \
+  do {                   \
+  } while (0)
+#define PLH_CWAVE_END(g) \
+  do {                   \
   } while (0)
 #endif
 
@@ -810,6 +841,7 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
   }
   lo = uniform(lo);
   hi = uniform(hi);
+  PLH_CSTAMP(g, 2);
   double theta = -INFINITY;
   if (hi > -INFINITY) {
     const Affine af = make_affine(lo, hi, kHB);
@@ -843,6 +875,7 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
     if (d >= 0) theta = d > 0 ? tlo + ((double)d - tmargin) / tscale : lo;
   }
   theta = uniform(theta);
+  PLH_CSTAMP(g, 3);
   const TIn tin = in_threshold<TIn>(theta);
   // lane 0 holds the most pool entries (entry i is on lane i mod 64)
   const int npw = uniform(tk.np);
@@ -858,6 +891,7 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
   int base = 0;
   if (lane() == 0) base = lds_fetch_add(&cm.cand_n, wtot);
   base = lane_value(base, 0);
+  PLH_CSTAMP(g, 4);
   // the wave's candidates go to its slots [base, base + wtot) in LDS first,
   // then to the workspace with consecutive lanes on consecutive slots; a
   // wave whose slots would run past capc makes the chunk incomplete
@@ -912,7 +946,9 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
       }
     }
   }
+  PLH_CSTAMP(g, 5);
   if (bucket) write_buckets<TIn>(a, g, hi, invT, cm);
+  PLH_CSTAMP(g, 6);
   // every token left out is below theta
   if (lane() == 0) {
     wp->zmax = hi;
@@ -922,11 +958,6 @@ __device__ __forceinline__ void chunk_candidates(ChunkToks<TIn>& tk, double lmax
   }
 }
 
-// Chunk index (row * C + chunk) of a block of the B x C chunk grids.  The
-// hardware deals block ids to the 8 XCDs round robin (block b to XCD b % 8);
-// the blocks of one row all carry the same b % 8, so a row's chunks and its
-// merge (block `row` of the per-row grids) share one XCD's L2.  -1: a
-// padding block (B not a multiple of 8).
 // Nucleus bins lie on power-of-two grids: with rz = 2^e bins per unit of z,
 // a token's bin is floor(zf * rz) for zf its z rounded to float (zf * rz is
 // exact, so the bins are exact half-open intervals of zf, monotone in z).
@@ -957,6 +988,11 @@ __device__ __forceinline__ NucGrid nuc_fit(float lo, float hi) {
 // The exponent of a power-of-two float.
 __device__ __forceinline__ int pow2_exp(float rz) { return ((__float_as_int(rz) >> 23) & 0xff) - 127; }
 
+// Chunk index (row * C + chunk) of a block of the B x C chunk grids.  The
+// hardware deals block ids to the 8 XCDs round robin (block b to XCD b % 8);
+// the blocks of one row all carry the same b % 8, so a row's chunks and its
+// merge (block `row` of the per-row grids) share one XCD's L2.  -1: a
+// padding block (B not a multiple of 8).
 constexpr int kXcds = 8;
 __device__ __forceinline__ int chunk_block(int C, int B) {
   const int x = (int)blockIdx.x % kXcds, k = (int)blockIdx.x / kXcds;
@@ -977,6 +1013,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
   const int C = a.ws.C;
   const int g = chunk_block(C, a.B);
   if (g < 0) return;
+  PLH_CSTAMP(g, 0);
   const int row = g / C;
   const int c0 = (g - row * C) * G::kChunk;
   // the row's parameters as vector loads, in flight with the chunk's (a
@@ -1015,11 +1052,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     if (first < G::kEpt) best = ArgMax{(double)m, c0 + slot_q<TIn>(first)};
     for (int i = 0; i < tk.np; ++i) best = argmax_merge(best, ArgMax{tk.pen_z(cm, i), tk.pen_tok(cm, i)});
     best = wave_argmax(best);
+    PLH_CSTAMP(g, 1);
     if (lane() == 0) {
       wp->best_z = best.v;
       wp->best_idx = best.i;
       wp->flags = flags;
     }
+    PLH_CSTAMP(g, 7);
+    PLH_CWAVE_END(g);
     return;
   }
   const double* tab = cm.exp_tab[wave()];
@@ -1042,6 +1082,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     for (int e = 0; e < G::kEpt; e += 2) m1 = in_max3(m1, tk.rv(e), tk.rv(e + 1));
   }
   double lmax = (double)m1;
+  PLH_CSTAMP(g, 1);
   for (int i = 0; i < tk.np; ++i) lmax = fmax(lmax, tk.pen_z(cm, i));
   // lane 0 holds the most pool entries: none there means the wave's
   // tokens are all in the registers, in the input precision
@@ -1125,6 +1166,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
       a.ws.seg_s[(size_t)g * kWaves + wave()] = s;
     }
   }
+  PLH_CSTAMP(g, 7);
+  PLH_CWAVE_END(g);
 }
 
 // ================================================================ finish
@@ -3407,5 +3450,14 @@ hipError_t launch_penalize(const PenalizeArgs& a, bool f64, hipStream_t s) {
 // row, shader clock ticks) to host memory.
 extern "C" int plh_phase_stamps(unsigned long long* host) {
   return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(plh::g_phase), sizeof(plh::g_phase));
+}
+// Profiling build only: k_sample_chunks' stamps of chunks 0..4095: phase
+// clocks (8 a chunk), real-time clocks (the start, then each wave's end: 9 a
+// chunk) and hardware ids (HW_ID, XCC_ID: 2 a chunk).
+extern "C" int plh_chunk_stamps(unsigned long long* phase, unsigned long long* rt, unsigned int* hw) {
+  hipError_t e = hipMemcpyFromSymbol(phase, HIP_SYMBOL(plh::g_cphase), sizeof(plh::g_cphase));
+  if (e == hipSuccess) e = hipMemcpyFromSymbol(rt, HIP_SYMBOL(plh::g_crt), sizeof(plh::g_crt));
+  if (e == hipSuccess) e = hipMemcpyFromSymbol(hw, HIP_SYMBOL(plh::g_chw), sizeof(plh::g_chw));
+  return (int)e;
 }
 #endif
