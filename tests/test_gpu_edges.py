@@ -184,3 +184,52 @@ def test_logits_far_from_zero(offset):
     print(f"offset {offset}: general-path rows {f2 - f1} (near zero: {f1 - f0})", flush=True)
     assert f2 - f1 <= f1 - f0 + 4
     assert ids0.shape == ids.shape
+
+
+def test_clustered_top_p_rows():
+    """Top-p rows whose large values cluster inside the threads' register
+    slots (values repeated in blocks of 4, 16 or 256 tokens, sorted rows),
+    where a threshold taken from a few values per thread would keep far too
+    many candidates.  Ids match the oracle, and the block rows stay on the
+    fast path: the chunk's value histogram keeps ~965-995 candidates of the
+    1024 slots on them, as on unclustered rows.  The sorted rows hold their
+    whole nucleus in one chunk and go to the general pipeline."""
+    from pagellm_amd import _native
+
+    g = np.random.default_rng(77)
+    V, B = 65536, 12
+    rows = []
+    for b in range(B):
+        kind = b % 6
+        if kind == 0:
+            r = np.repeat(g.normal(0, 3, V // 4), 4)
+        elif kind == 1:
+            r = np.repeat(g.normal(0, 3, V // 16), 16)
+        elif kind == 2:
+            r = np.repeat(g.normal(0, 3, V // 256), 256) + g.normal(0, 0.01, V)
+        elif kind == 3:
+            r = g.normal(0, 3, V)  # control: no clustering
+        elif kind == 4:
+            r = np.sort(g.normal(0, 3, V))
+        else:
+            r = np.sort(g.normal(0, 3, V))[::-1].copy()
+        rows.append(r)
+    x = np.stack(rows).astype(np.float32)
+    # nuclei that fit the slots (top_p 0.95 over N(0, 3^2) rows would need
+    # ~1440 candidates a chunk: the general pipeline with either threshold)
+    params = [SamplingParams(top_p=[0.9, 0.8, 0.5][b % 3], repetition_penalty=1.0 if b < 6 else 1.2) for b in range(B)]
+    ctx = [list(g.integers(0, V, 200)) for _ in range(B)]
+    u = g.random(B)
+    c = _native.default_context()
+    block_rows = [b for b in range(B) if b % 6 in (0, 1, 2, 3)]
+    f0 = c.fallback_rows()
+    ids_blocks = sample_batch(x[block_rows], [params[b] for b in block_rows], uniforms=u[block_rows],
+                              contexts=[ctx[b] for b in block_rows])
+    f1 = c.fallback_rows()
+    ids = sample_batch(x, params, uniforms=u, contexts=ctx)
+    f2 = c.fallback_rows()
+    _check(x, params, u, ctx, ids)
+    assert list(ids_blocks) == [int(ids[b]) for b in block_rows]
+    print(f"clustered rows: general-path rows {f1 - f0} of {len(block_rows)} block rows, {f2 - f1} of {B} in all",
+          flush=True)
+    assert f1 - f0 == 0
