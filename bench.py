@@ -471,7 +471,7 @@ def phase_stamps(steps: int = 6) -> dict:
     d = {n: torch.from_numpy(a).to(dev) for n, a in
          dict(t=t, k=k, p=p, r=r, u=w["uniforms"], ids=hist_ids, off=hist_off).items()}
     out = torch.empty(B, dtype=torch.int32, device=dev)
-    runs, cruns = [], []
+    runs, cruns, fruns = [], [], []
     C = (V + 16383) // 16384  # 64 KB chunks of float32
     for _ in range(steps):
         ctx.sample(x.data_ptr(), _native.PLH_F32, V, B, V, d["ids"].data_ptr(), d["off"].data_ptr(),
@@ -488,10 +488,24 @@ def phase_stamps(steps: int = 6) -> dict:
         cruns.append((np.frombuffer(cph, dtype=np.uint64).reshape(4096, 8).astype(np.int64),
                       np.frombuffer(crt, dtype=np.uint64).reshape(4096, 9).astype(np.int64),
                       np.frombuffer(chw, dtype=np.uint32).reshape(4096, 2).astype(np.int64)))
+        frt = (ctypes.c_ulonglong * (256 * 2))()
+        if ctx.lib.plh_final_rt(frt) != 0:
+            raise SystemExit("plh_final_rt failed")
+        fruns.append(np.frombuffer(frt, dtype=np.uint64).reshape(256, 2).astype(np.int64))
     ctx.close()
     a = np.stack(runs[1:])
     res = {"workload": "mixed128k", "unit": "shader clock ticks from the workgroup's start", "groups": {},
-           "chunk_groups": {}, "chunk_timeline": [chunk_timeline(*r, B, C) for r in cruns[1:]]}
+           "chunk_groups": {}, "chunk_timeline": [chunk_timeline(*r, B, C) for r in cruns[1:]],
+           "final_timeline": []}
+    for (cp_, crt_, _), frt_ in zip(cruns[1:], fruns[1:]):
+        chunk_end = crt_[:B * C, 1:].max()
+        f0, f1 = frt_[:B, 0], frt_[:B, 1]
+        life = f1 - f0
+        res["final_timeline"].append({
+            "gap_us_chunk_last_wave_to_first_merge_start": round(float(f0.min() - chunk_end) * 0.01, 2),
+            "span_us": round(float(f1.max() - f0.min()) * 0.01, 2),
+            "start_spread_us": round(float(f0.max() - f0.min()) * 0.01, 2),
+            "life_us_median_per_group": [round(float(np.median(life[64 * g:64 * g + 64])) * 0.01, 2) for g in range(4)]})
     cph = np.stack([r[0][:B * C] for r in cruns[1:]])
     for g in range(4):
         blk = cph[:, 64 * g * C:64 * (g + 1) * C, :]

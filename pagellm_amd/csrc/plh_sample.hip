@@ -40,7 +40,8 @@ namespace plh {
 
 // Phase clock stamps of k_sample_final and k_sample_chunks, in a profiling build only
 // (-DPLH_PHASE_STAMPS: python -m pagellm_amd.build --phase-stamps): thread
-// 0 of row r's workgroup records the shader clock on reaching phase k
+// 0 of row r's workgroup records the shader clock on reaching phase k (and
+// the real-time clock at its start and end)
 // (0 start, 1 wave parts, 2 normaliser, 3 row buckets, 4 cut-bucket entries
 // loaded, 5 cut selected, 6 per-chunk kept sums, 7 draw bins, 8 draw bin
 // scattered, 9 end; 10-13 the mass selection: start, first level's
@@ -48,10 +49,13 @@ namespace plh {
 #ifdef PLH_PHASE_STAMPS
 constexpr int kStampRows = 256, kStampSlots = 16;
 __device__ unsigned long long g_phase[kStampRows * kStampSlots];
-#define PLH_STAMP(row, k)                                                 \
-  do {                                                                    \
-    if (threadIdx.x == 0 && (row) < kStampRows)                           \
-      g_phase[(row) * kStampSlots + (k)] = __builtin_readcyclecounter(); \
+__device__ unsigned long long g_frt[kStampRows * 2];  // real-time clock at phases 0 and 9
+#define PLH_STAMP(row, k)                                                                                   \
+  do {                                                                                                      \
+    if (threadIdx.x == 0 && (row) < kStampRows) {                                                           \
+      g_phase[(row) * kStampSlots + (k)] = __builtin_readcyclecounter();                                    \
+      if ((k) == 0 || (k) == 9) g_frt[(row) * 2 + ((k) == 9 ? 1 : 0)] = __builtin_amdgcn_s_memrealtime(); \
+    }                                                                                                       \
   } while (0)
 #define PLH_STAMP_IF(c, row, k) \
   do {                          \
@@ -3450,6 +3454,11 @@ hipError_t launch_penalize(const PenalizeArgs& a, bool f64, hipStream_t s) {
 // row, shader clock ticks) to host memory.
 extern "C" int plh_phase_stamps(unsigned long long* host) {
   return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(plh::g_phase), sizeof(plh::g_phase));
+}
+// Profiling build only: k_sample_final's real-time clocks (start, end) of
+// rows 0..255.
+extern "C" int plh_final_rt(unsigned long long* host) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(plh::g_frt), sizeof(plh::g_frt));
 }
 // Profiling build only: k_sample_chunks' stamps of chunks 0..4095: phase
 // clocks (8 a chunk), real-time clocks (the start, then each wave's end: 9 a
