@@ -118,6 +118,41 @@ def test_instructions_per_token_per_kernel(tmp_path):
     assert (tmp_path / "k.json").exists()
 
 
+def test_chunk_timeline_from_stamps():
+    """--phase-stamps: the chunk pass's timeline from its real-time stamps.
+    Two CUs with two slots each run three workgroups a slot, back to back
+    with a 20-count gap; the clock rate, the span, the lifetimes, the
+    residency and the refill gap come out as constructed."""
+    import numpy as np
+
+    import bench
+
+    B, C = 3, 4  # 12 chunks: 2 CUs x 2 slots x 3 in turn
+    n = B * C
+    ph = np.zeros((4096, 8), np.int64)
+    rt = np.zeros((4096, 9), np.int64)
+    hw = np.zeros((4096, 2), np.int64)
+    life, gap = 100, 20
+    for g in range(n):
+        cu, slot, k = g % 2, (g // 2) % 2, g // 4
+        t0 = k * (life + gap)
+        rt[g, 0] = t0
+        rt[g, 1:] = t0 + life - 5  # waves 0..6 end 5 counts early
+        rt[g, 8] = t0 + life  # the last wave
+        ph[g, 0], ph[g, 7] = 1000, 1000 + 22 * (life - 5)  # 2.2 GHz: 22 clocks a 10 ns count
+        hw[g, 0] = cu << 8  # CU id bits 11:8 of HW_ID
+        hw[g, 1] = 0
+    t = bench.chunk_timeline(ph, rt, hw, B, C)
+    assert t["cus"] == 2
+    assert t["clock_ghz"] == pytest.approx(2.2)
+    assert t["span_us"] == pytest.approx((2 * (life + gap) + life) * 0.01)
+    assert t["workgroup_life_us_median"] == pytest.approx(life * 0.01)
+    assert t["slot_refill_gap_us_median"] == pytest.approx(gap * 0.01)
+    assert t["wave0_end_to_last_wave_end_us_median"] == pytest.approx(5 * 0.01)
+    # 12 lives of 100 over 2 CUs x a span of 340
+    assert t["resident_workgroups_per_cu_mean"] == pytest.approx(round(12 * life / (2 * 340), 2))
+
+
 def test_algorithmic_bytes_of_the_headline_workload():
     """4V per row of fp32 logits, 4H per history id of a penalised row, 48
     per row of parameters, uniform, offset and id."""
