@@ -76,7 +76,7 @@ def _parity_rows(w, rows, gpu_ids):
     """Oracle ids for the given rows against the GPU's, with the boundary
     gauges for every row: greedy rows must agree exactly; a sampled row may
     differ only if its uniform lies within 1e-6 of a CDF boundary or its
-    top-p cut within 1e-12 of flipping (the north-star band), and the
+    top-p cut within 1e-12 of flipping (the 1e-6 boundary rule), and the
     kernels' fixed-point CDF keeps every mismatch within 1e-12 of one
     (``mismatches_outside_1e-12`` counts those that are not)."""
     import oracle

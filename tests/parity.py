@@ -11,7 +11,7 @@ V = 152 064. The tests therefore hold ids to a 1e-12 band:
   ``sampling.py:94-98`` and ``:84-92``);
 * speculative accept/resample decisions are held to the same 1e-12 band;
 * rows whose uniform lies within ``BAND`` = 1e-6 of a CDF boundary are
-  counted and printed, the count the north-star bar asks for, whether or
+  counted and printed (the count the 1e-6 boundary rule reports), whether or
   not the ids agree.
 """
 
