@@ -395,7 +395,8 @@ def traffic_from(workload: str, fetch_dir: str, write_dir: str, dst: Path | None
 
 
 PHASES = {0: "start", 1: "wave parts", 2: "normaliser", 3: "row buckets", 4: "cut-bucket entries loaded",
-          10: "mass selection start", 11: "first level histogram", 12: "rank list", 13: "ranked",
+          10: "mass selection start", 14: "level bins counted", 15: "level barrier passed",
+          11: "level pick", 12: "rank list", 13: "ranked",
           5: "cut selected", 6: "per-chunk kept sums", 7: "draw bins", 8: "draw bin scattered", 9: "end"}
 
 

@@ -44,8 +44,9 @@ namespace plh {
 // the real-time clock at its start and end)
 // (0 start, 1 wave parts, 2 normaliser, 3 row buckets, 4 cut-bucket entries
 // loaded, 5 cut selected, 6 per-chunk kept sums, 7 draw bins, 8 draw bin
-// scattered, 9 end; 10-13 the mass selection: start, first level's
-// histogram, rank list, ranked).  The default build compiles them out.
+// scattered, 9 end; 10-15 the mass selection: start, a level's pick, rank
+// list, ranked, a level's bins counted (thread 0), the level's barrier
+// passed).  The default build compiles them out.
 #ifdef PLH_PHASE_STAMPS
 constexpr int kStampRows = 256, kStampSlots = 16;
 __device__ unsigned long long g_phase[kStampRows * kStampSlots];
@@ -2100,7 +2101,9 @@ __device__ __forceinline__ ZSel select_z(uint32_t act, const MCands& mc, double 
         if (MASS) lds_add(&h.mass[b], mc.w[j]);
       }
     }
+    PLH_STAMP_IF(MASS, (int)blockIdx.x, 14);
     wg_barrier();
+    PLH_STAMP_IF(MASS, (int)blockIdx.x, 15);
     const WPick pk = wave_pick2<MASS>(h, above, target);
     PLH_STAMP_IF(MASS, (int)blockIdx.x, 11);
     if (!pk.found) return ZSel{false, false, 0.0, 0};
