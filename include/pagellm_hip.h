@@ -69,7 +69,11 @@ int plh_create(plh_ctx** out, int device);
 void plh_destroy(plh_ctx* ctx);
 const char* plh_last_error(const plh_ctx* ctx);
 /* Queue work on `stream` (a hipStream_t, e.g. torch's current stream); NULL
- * restores the context's own stream. */
+ * restores the context's own stream.  Moving to another stream records an
+ * event on the stream being left that closes the calls queued there; the
+ * next call on the new stream waits for it (calls on one stream record
+ * nothing).  A stream stays in use until the context moves off it or is
+ * destroyed: it must stay valid until then. */
 int plh_set_stream(plh_ctx* ctx, void* stream);
 int plh_set_option(plh_ctx* ctx, int option, int64_t value);
 /* Rows the fast path (its merge kernel or the nucleus kernels) finished with

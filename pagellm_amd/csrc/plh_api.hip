@@ -19,18 +19,23 @@ struct plh_ctx {
   hipStream_t own_stream = nullptr;
   hipStream_t stream = nullptr;
   unsigned long long* fallback = nullptr;
-  // fast-path workspace, reused by every call on this context; ws_done marks
-  // the end of the last call that used it (on ws_stream)
+  // fast-path workspace, reused by every call on this context.  ws_stream:
+  // the stream of the last call that used it; ws_open: that call is not yet
+  // closed by ws_done, which plh_set_stream records on the stream it leaves
+  // (one event per stream change instead of one per call: an event record
+  // costs the queue ~3 us per two-kernel step)
   void* ws = nullptr;
   size_t ws_bytes = 0;
   hipEvent_t ws_done = nullptr;
   hipStream_t ws_stream = nullptr;
+  bool ws_open = false;
   // plh_sample_noalloc: this device's copy of the file-scope scratch array;
-  // scratch_done marks the end of this context's last noalloc call (on
-  // scratch_stream)
+  // scratch_stream, scratch_open and scratch_done as above, for this
+  // context's noalloc calls
   void* scratch = nullptr;
   hipEvent_t scratch_done = nullptr;
   hipStream_t scratch_stream = nullptr;
+  bool scratch_open = false;
   // PLH_OPT_KERNEL_TIMING: event triples (start, between, end) per timed call
   bool timing = false;
   std::vector<hipEvent_t> ev_free;
@@ -87,6 +92,7 @@ int reserve_ws(plh_ctx* c, size_t bytes) {
     PLH_HIP(c, hipMalloc(&c->ws, sz), "hipMalloc(workspace)");
     c->ws_bytes = sz;
     c->ws_stream = nullptr;
+    c->ws_open = false;
   }
   if (c->ws_stream != nullptr && c->ws_stream != c->stream)
     PLH_HIP(c, hipStreamWaitEvent(c->stream, c->ws_done, 0), "hipStreamWaitEvent");
@@ -216,8 +222,8 @@ int sample_impl(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, in
     a.ws = plh::fast_ws_layout(c->scratch, B, V, f64);
     const hipError_t e = plh::launch_sample_fast(a, f64, vec, c->num_cu, c->stream, nullptr);
     if (e != hipSuccess) return hip_fail(c, e, "plh_sample_noalloc launch");
-    PLH_HIP(c, hipEventRecord(c->scratch_done, c->stream), "hipEventRecord");
     c->scratch_stream = c->stream;
+    c->scratch_open = true;
     return PLH_OK;
   }
   rc = reserve_ws(c, need);
@@ -229,8 +235,8 @@ int sample_impl(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, in
   const hipError_t e = plh::launch_sample_fast(a, f64, vec, c->num_cu, c->stream, ev[1]);
   if (e != hipSuccess) return hip_fail(c, e, "plh_sample launch");
   if (c->timing) PLH_HIP(c, hipEventRecord(ev[2], c->stream), "hipEventRecord");
-  PLH_HIP(c, hipEventRecord(c->ws_done, c->stream), "hipEventRecord");
   c->ws_stream = c->stream;
+  c->ws_open = true;
   return PLH_OK;
 }
 
@@ -290,7 +296,24 @@ const char* plh_last_error(const plh_ctx* c) { return c == nullptr ? "null conte
 
 int plh_set_stream(plh_ctx* c, void* stream) {
   if (c == nullptr) return PLH_ERR_INVALID_ARG;
-  c->stream = stream != nullptr ? static_cast<hipStream_t>(stream) : c->own_stream;
+  const hipStream_t s = stream != nullptr ? static_cast<hipStream_t>(stream) : c->own_stream;
+  if (s == c->stream) return PLH_OK;
+  // leaving a stream: an event closes the calls queued on it that used the
+  // workspace or the scratch array; the next such call on another stream
+  // waits for it (reserve_ws, order_scratch)
+  if (c->ws_open || c->scratch_open) {
+    const int rc = use_device(c);
+    if (rc != PLH_OK) return rc;
+  }
+  if (c->ws_open && c->ws_stream == c->stream) {
+    PLH_HIP(c, hipEventRecord(c->ws_done, c->stream), "hipEventRecord");
+    c->ws_open = false;
+  }
+  if (c->scratch_open && c->scratch_stream == c->stream) {
+    PLH_HIP(c, hipEventRecord(c->scratch_done, c->stream), "hipEventRecord");
+    c->scratch_open = false;
+  }
+  c->stream = s;
   return PLH_OK;
 }
 
@@ -516,8 +539,8 @@ int plh_verify(plh_ctx* c, const void* p, const void* q, int dtype, int B, int k
   const hipError_t e = plh::launch_verify(a, ws, dtype == PLH_F64, c->stream, ev[1]);
   if (e != hipSuccess) return hip_fail(c, e, "plh_verify launch");
   if (c->timing) PLH_HIP(c, hipEventRecord(ev[2], c->stream), "hipEventRecord");
-  PLH_HIP(c, hipEventRecord(c->ws_done, c->stream), "hipEventRecord");
   c->ws_stream = c->stream;
+  c->ws_open = true;
   return PLH_OK;
 }
 
@@ -576,8 +599,8 @@ int plh_rmsnorm_lm_head(plh_ctx* c, const float* h, int64_t ldh, int N, int D, c
   a.V = V;
   const hipError_t e = plh::launch_head(a, c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "plh_rmsnorm_lm_head launch");
-  PLH_HIP(c, hipEventRecord(c->ws_done, c->stream), "hipEventRecord");
   c->ws_stream = c->stream;
+  c->ws_open = true;
   return PLH_OK;
 }
 

@@ -202,3 +202,63 @@ def test_penalize_rejects_in_place_and_overlapping_output():
     with pytest.raises(ValueError, match="overlap"):  # out's row 0 reaches one element into x's row 1
         c.penalize(d_buf.ptr, _native.PLH_F32, 2 * V, B, V, d_ids.ptr, d_off.ptr, d_pen.ptr,
                    d_buf.ptr + 4 * (V + 1), 2 * V)
+
+
+def _launch_rows(c, w, rows=None):
+    """plh_sample on the context's current stream, not waited for: the
+    device ids (their inputs kept alive with them)."""
+    from pagellm_amd.sampling import _nucleus_hint, _pack_histories
+
+    x = w["logits"] if rows is None else w["logits"][:rows]
+    params = w["params"] if rows is None else w["params"][:rows]
+    ctxs = w["contexts"] if rows is None else w["contexts"][:rows]
+    u = w["uniforms"] if rows is None else w["uniforms"][:rows]
+    B, V = x.shape
+    t, k, p, r = _pack_params(params)
+    hist_ids, hist_off = _pack_histories(ctxs, params, B, V)
+    d = {n: c.to_device(a) for n, a in dict(x=x, t=t, k=k, p=p, r=r, u=u).items()}
+    hi = c.to_device(hist_ids) if hist_ids is not None else None
+    ho = c.to_device(hist_off) if hist_off is not None else None
+    out = c.empty((B,), np.int32)
+    c.sample(d["x"].ptr, _native.dtype_code(x.dtype), V, B, V, hi.ptr if hi else None, ho.ptr if ho else None,
+             d["t"].ptr, d["k"].ptr, d["p"].ptr, d["r"].ptr, d["u"].ptr, out.ptr, None, _nucleus_hint(t, k, p, V))
+    out.keep = (d, hi, ho)
+    return out
+
+
+def test_workspace_calls_on_changing_streams():
+    """plh_sample calls of one context share its workspace.  Calls on one
+    stream record no event; moving to another stream closes the calls on
+    the stream left, and the next call waits for them.  Back-to-back calls
+    with no host wait, switching streams between them (and once right after
+    the workspace grew), return the ids of calls made one at a time."""
+    import torch
+
+    from pagellm_amd import workloads
+
+    c = _native.Context(0)
+    try:
+        small, big = workloads.zipf32k(), workloads.mixed128k()
+        ref_small = _launch_rows(c, small, rows=48).download()
+        ref_big = _launch_rows(c, big).download()
+        c.close()
+        c = _native.Context(0)  # a fresh context: its workspace grows on the way
+        s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+        outs = []
+        c.set_stream(s1.cuda_stream)
+        outs.append((_launch_rows(c, small, rows=48), ref_small))
+        outs.append((_launch_rows(c, small, rows=48), ref_small))  # same stream: no event
+        c.set_stream(s2.cuda_stream)
+        outs.append((_launch_rows(c, big), ref_big))  # grows the workspace after s1's calls
+        c.set_stream(s1.cuda_stream)
+        outs.append((_launch_rows(c, small, rows=48), ref_small))
+        c.set_stream(None)
+        outs.append((_launch_rows(c, big), ref_big))
+        c.set_stream(s2.cuda_stream)
+        outs.append((_launch_rows(c, small, rows=48), ref_small))
+        torch.cuda.synchronize()
+        for i, (o, ref) in enumerate(outs):
+            assert np.array_equal(o.download(), ref), i
+    finally:
+        c.set_stream(None)
+        c.close()
