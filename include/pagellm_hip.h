@@ -77,8 +77,8 @@ const char* plh_last_error(const plh_ctx* ctx);
 int plh_set_stream(plh_ctx* ctx, void* stream);
 int plh_set_option(plh_ctx* ctx, int option, int64_t value);
 /* Rows the fast path (its merge kernel or the nucleus kernels) finished with
- * the general row-wise pipeline, cumulative since plh_create (waits for
- * queued work). */
+ * the general row-wise pipeline, cumulative since plh_create (waits for the
+ * context's queued calls, on its stream and on the streams it left). */
 int plh_fallback_rows(plh_ctx* ctx, int64_t* out);
 /* While PLH_OPT_KERNEL_TIMING is on: device time of the fast path's
  * streaming kernel and merge kernel summed over the plh_sample calls made

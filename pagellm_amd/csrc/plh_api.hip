@@ -357,6 +357,11 @@ int plh_fallback_rows(plh_ctx* c, int64_t* out) {
   if (c == nullptr || out == nullptr) return PLH_ERR_INVALID_ARG;
   int rc = use_device(c);
   if (rc != PLH_OK) return rc;
+  // this context's calls on a stream it has left are closed by their events
+  if (c->ws_stream != nullptr && c->ws_stream != c->stream)
+    PLH_HIP(c, hipStreamWaitEvent(c->stream, c->ws_done, 0), "hipStreamWaitEvent");
+  if (c->scratch_stream != nullptr && c->scratch_stream != c->stream)
+    PLH_HIP(c, hipStreamWaitEvent(c->stream, c->scratch_done, 0), "hipStreamWaitEvent");
   unsigned long long v = 0;
   PLH_HIP(c, hipMemcpyAsync(&v, c->fallback, sizeof(v), hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync");
   PLH_HIP(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
