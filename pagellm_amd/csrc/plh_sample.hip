@@ -2642,6 +2642,7 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   PartLoad pl;
   load_parts_first(a, row, pl);
   const RowParams rp = row_params_of(a, rload);
+  if (NUC && rp.nucleus) return;  // the nucleus kernels own the row (k_nuc_window onwards)
   init_exp_table_wave(fs.exp_tab[wave()]);
   const bool cands = !rp.greedy && (rp.topk || (rp.topp && !(NUC && rp.nucleus)));
   if (cands) {  // ordered before their first use by the first barrier
@@ -2679,46 +2680,6 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
   bool general = ps.flags != 0;
   int id = 0;
   PipeIn pin{false, 0.0, false, 0.0, false, 0.0};  // what the fast path already knows of the row
-  if (NUC && rp.nucleus) {
-    if (general) {
-      if (threadIdx.x == 0) a.ws.nrow[row].state = 0;  // finished here: the nucleus kernels skip it
-    } else {
-      // the nucleus kernels finish the row; its bins span the row's finite
-      // penalised logits on a power-of-two grid no finer than any chunk's
-      if (wave() == 0) {
-        const int C = a.ws.C;
-        const WavePart* pp = a.ws.part + (size_t)row * C * kWaves;
-        double lo = INFINITY, hi = -INFINITY;
-        for (int j = lane(); j < C * kWaves; j += kWave) {
-          lo = fmin(lo, pp[j].umax);  // nucleus rows: the wave's smallest finite logit
-          hi = fmax(hi, pp[j].zmax);
-        }
-        float crz = INFINITY;
-        int bad = 0;
-        for (int j = lane(); j < C; j += kWave) {
-          const float r = a.ws.ngrid[(size_t)row * C + j].rz;
-          if (r < 0.0f) bad = 1;
-          if (r > 0.0f) crz = fminf(crz, r);
-        }
-        lo = wave_min(lo);
-        hi = wave_max(hi);
-        crz = wave_min(crz);
-        bad = wave_max(bad);
-        if (lane() == 0) {
-          const NucGrid rg = nuc_fit((float)lo, (float)hi);
-          const float rz = fminf(rg.rz, crz);
-          NucRow& nr = a.ws.nrow[row];
-          nr.rz = rz;
-          nr.base = rz > 0.0f ? __float2int_rd((float)lo * rz) : 0;
-          // one distinct finite value, or none, or logits too large to bin:
-          // the general pipeline (k_nuc_final)
-          nr.general = (hi - lo > 0.0 && hi - lo < INFINITY && rg.rz > 0.0f && !bad) ? 0 : 1;
-          nr.state = kNucActive;
-        }
-      }
-      return;
-    }
-  }
   if (general) {
   } else if (rp.greedy) {
     id = ps.best.i;
@@ -2755,9 +2716,11 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
 // finite logit, (penalised rows) each chunk's bitmap of penalised tokens,
 // and each chunk's count histogram on a power-of-two grid of its own (the
 // finest that fits the chunk's range in kNucBins bins); k_sample_final
-// picks the row's grid, no finer than any chunk's (or finishes the row
-// itself when a chunk could not set its penalised tokens aside); then
-//   k_nuc_window  adds the chunks' histograms into the row's bins and
+// leaves such rows at once; then
+//   k_nuc_window  picks the row's grid, no finer than any chunk's (or hands
+//                 the row to the general pipeline when a chunk could not set
+//                 its penalised tokens aside), adds the chunks' histograms
+//                 into the row's bins and
 //                 bounds each bin's mass by its count and the exp of its
 //                 edges, which brackets the top-p cut (sampling.py:82-90) in a
 //                 window of bins: the bins below it hold at most 1 - top_p
@@ -2770,7 +2733,42 @@ __global__ __launch_bounds__(kThreads) void k_sample_final(SampleArgs a) {
 //                 (sampling.py:94-98): the segment where the kept mass
 //                 crosses u * total, rescanned from HBM.
 // A row whose window does not fit its candidate slots, or whose cut falls
-// outside the window, is finished by the general pipeline.
+// outside the window, is finished by the general pipeline (in k_nuc_final).
+
+// A nucleus row's grid, by every wave on its own from the same data (the
+// same result in each): its bins span the row's finite penalised logits on
+// a power-of-two grid no finer than any chunk's.  general: a chunk could not
+// set its penalised tokens aside, or the row has one distinct finite value,
+// none, or logits too large to bin (the general pipeline, k_nuc_final).
+__device__ __forceinline__ void nuc_row_grid(const SampleArgs& a, int row, float* rz_out, int* base_out,
+                                             int* general_out) {
+  const int C = a.ws.C;
+  const WavePart* pp = a.ws.part + (size_t)row * C * kWaves;
+  double lo = INFINITY, hi = -INFINITY;
+  int flags = 0;
+  for (int j = lane(); j < C * kWaves; j += kWave) {
+    const WavePart w = pp[j];
+    lo = fmin(lo, w.umax);  // nucleus rows: the wave's smallest finite logit
+    hi = fmax(hi, w.zmax);
+    flags |= w.flags;
+  }
+  float crz = INFINITY;
+  int bad = 0;
+  for (int j = lane(); j < C; j += kWave) {
+    const float r = a.ws.ngrid[(size_t)row * C + j].rz;
+    if (r < 0.0f) bad = 1;
+    if (r > 0.0f) crz = fminf(crz, r);
+  }
+  lo = wave_min(lo);
+  hi = wave_max(hi);
+  crz = wave_min(crz);
+  bad = wave_max(bad | (flags != 0 ? 1 : 0));
+  const NucGrid rg = nuc_fit((float)lo, (float)hi);
+  const float rz = fminf(rg.rz, crz);
+  *rz_out = rz;
+  *base_out = rz > 0.0f ? __float2int_rd((float)lo * rz) : 0;
+  *general_out = (hi - lo > 0.0 && hi - lo < INFINITY && rg.rz > 0.0f && !bad) ? 0 : 1;
+}
 
 // Bin of a nucleus row's token on the row's grid (NucRow rz, base), clamped
 // to [0, kNucBins - 1].  Every kernel that bins a token uses this function.
@@ -2837,8 +2835,17 @@ __global__ __launch_bounds__(kThreads) void k_nuc_window(SampleArgs a) {
   const int row = blockIdx.x;
   const RowParams rp = load_row_params(a, row);
   if (!rp.nucleus) return;
-  const NucRow nr = a.ws.nrow[row];
-  if (nr.state != kNucActive || nr.general != 0) return;
+  NucRow nr{};
+  nuc_row_grid(a, row, &nr.rz, &nr.base, &nr.general);
+  nr.state = kNucActive;
+  if (threadIdx.x == 0) {  // for k_nuc_cands and k_nuc_final (the window's fields follow below)
+    NucRow& g = a.ws.nrow[row];
+    g.rz = nr.rz;
+    g.base = nr.base;
+    g.general = nr.general;
+    g.state = kNucActive;
+  }
+  if (nr.general != 0) return;
   init_exp_table_wave(sm.exp_tab[wave()]);
   const double* tab = sm.exp_tab[wave()];
   constexpr int kPer = kNucBins / kThreads;
