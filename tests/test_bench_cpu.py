@@ -104,17 +104,17 @@ def test_instructions_per_token_per_kernel(tmp_path):
         w = csv.DictWriter(f, fieldnames=["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"])
         w.writeheader()
         for did, kern, v in ((1, "void plh::k_sample_chunks<float, true, true>(plh::SampleArgs)", 100.0),
-                             (2, "void plh::k_nuc_hist<float, true>(plh::SampleArgs)", 40.0),
+                             (2, "void plh::k_nuc_window<float>(plh::SampleArgs)", 40.0),
                              (3, "void plh::k_sample_chunks<float, true, true>(plh::SampleArgs)", 300.0),
                              (4, "void at::native::elementwise_kernel<128, 4>(int)", 1e9)):
             for c in ("SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_WAVES"):
                 w.writerow({"Dispatch_Id": did, "Kernel_Name": kern, "Counter_Name": c, "Counter_Value": v})
     out = bench.valu_kernels_from("zipf152k", str(tmp_path), dst=tmp_path / "k.json", shape=(B, V))
     ks = {k["kernel"]: k for k in out["kernels"]}
-    assert set(ks) == {"k_sample_chunks", "k_nuc_hist"}
+    assert set(ks) == {"k_sample_chunks", "k_nuc_window"}
     assert ks["k_sample_chunks"]["launches"] == 2
     assert ks["k_sample_chunks"]["valu_per_token"] == pytest.approx(200.0 * 64 / (B * V))
-    assert ks["k_nuc_hist"]["lds_per_token"] == pytest.approx(40.0 * 64 / (B * V))
+    assert ks["k_nuc_window"]["lds_per_token"] == pytest.approx(40.0 * 64 / (B * V))
     assert (tmp_path / "k.json").exists()
 
 
