@@ -262,3 +262,75 @@ def test_workspace_calls_on_changing_streams():
     finally:
         c.set_stream(None)
         c.close()
+
+
+def test_workspace_users_interleaved_on_streams():
+    """plh_sample, plh_verify and plh_rmsnorm_lm_head share the context's
+    workspace (each grows it to its own size).  Interleaved over three
+    streams with no host wait between the calls, every result equals the
+    same call made alone on one stream."""
+    import torch
+
+    from pagellm_amd import workloads
+
+    g = np.random.default_rng(11)
+    zw = workloads.zipf32k()
+    sw = workloads.spec32k()
+    Bv = 16
+    p, q = sw["p"][:Bv], sw["q"][:Bv]
+    draft = np.asarray(sw["draft"][:Bv], dtype=np.int32)
+    acc_u, res_u = sw["accept_u"][:Bv], sw["resample_u"][:Bv]
+    _, k1, V = p.shape
+    N, D, Vh = 8, 256, 3000
+    h = g.normal(0, 1, (N, D)).astype(np.float32)
+    norm = g.normal(1, 0.1, D).astype(np.float32)
+    wt = g.normal(0, 0.05, (D, Vh)).astype(np.float32)
+
+    def verify_call(c):
+        d = {n: c.to_device(a) for n, a in dict(p=p, q=q, d=draft, a=acc_u, w=res_u).items()}
+        tok, nacc = c.empty((Bv, k1), np.int32), c.empty((Bv,), np.int32)
+        c.verify(d["p"].ptr, d["q"].ptr, _native.PLH_F64, Bv, k1 - 1, V, d["d"].ptr, d["a"].ptr, d["w"].ptr, 0,
+                 tok.ptr, nacc.ptr)
+        tok.keep = nacc.keep = d
+        return tok, nacc
+
+    def head_call(c):
+        d = {n: c.to_device(a) for n, a in dict(h=h, n=norm, w=wt).items()}
+        out = c.empty((N, Vh), np.float32)
+        c.rmsnorm_lm_head(d["h"].ptr, D, N, D, d["n"].ptr, 1e-6, d["w"].ptr, Vh, Vh, out.ptr, Vh)
+        out.keep = d
+        return out
+
+    c = _native.Context(0)
+    try:
+        ref_s = _launch_rows(c, zw, rows=48).download()
+        ref_t, ref_n = (a.download() for a in verify_call(c))
+        ref_h = head_call(c).download()
+    finally:
+        c.close()
+    c = _native.Context(0)
+    try:
+        s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+        got = []
+        c.set_stream(s1.cuda_stream)
+        got.append(("head", head_call(c)))
+        c.set_stream(s2.cuda_stream)
+        got.append(("verify", verify_call(c)))
+        c.set_stream(None)
+        got.append(("sample", _launch_rows(c, zw, rows=48)))
+        c.set_stream(s1.cuda_stream)
+        got.append(("verify", verify_call(c)))
+        got.append(("head", head_call(c)))
+        c.set_stream(s2.cuda_stream)
+        got.append(("sample", _launch_rows(c, zw, rows=48)))
+        torch.cuda.synchronize()
+        for i, (kind, r) in enumerate(got):
+            if kind == "sample":
+                assert np.array_equal(r.download(), ref_s), i
+            elif kind == "verify":
+                assert np.array_equal(r[0].download(), ref_t) and np.array_equal(r[1].download(), ref_n), i
+            else:
+                assert np.array_equal(r.download(), ref_h), i
+    finally:
+        c.set_stream(None)
+        c.close()
