@@ -49,9 +49,14 @@ extern "C" {
                                    slots that grow in place (plh_append_ids) */
 #define PLH_SAMPLE_NUCLEUS 4 /* performance hint, same results: rows with no
                                 top-k and top_p >= 0.98 (nuclei that hold most
-                                of the vocabulary) take three streaming passes
+                                of the vocabulary) take two streaming passes
                                 over all chunks instead of the per-row general
-                                pipeline; costs four extra launches */
+                                pipeline; costs three extra launches */
+#define PLH_SAMPLE_NUCLEUS_ONLY 8 /* performance hint, same results, with
+                                     PLH_SAMPLE_NUCLEUS: every row is such a
+                                     row, so the merge kernel is not launched;
+                                     a row that is not one is finished by the
+                                     general pipeline in the nucleus path */
 
 /* plh_set_option options */
 #define PLH_OPT_KERNEL_TIMING 1 /* value 1: bracket the fast path's kernels with

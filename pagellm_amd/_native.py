@@ -27,6 +27,7 @@ PLH_F64 = 1
 PLH_SAMPLE_ROWWISE = 1
 PLH_SAMPLE_HIST_SPANS = 2
 PLH_SAMPLE_NUCLEUS = 4
+PLH_SAMPLE_NUCLEUS_ONLY = 8
 PLH_OPT_KERNEL_TIMING = 1
 
 _c_int, _c_i64, _c_sz, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p

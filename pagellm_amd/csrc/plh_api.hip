@@ -202,6 +202,7 @@ int sample_impl(plh_ctx* c, const void* logits, int dtype, int64_t ld, int B, in
   a.out_probs = out_probs;
   a.fallback_rows = c->fallback;
   a.nucleus = (flags & PLH_SAMPLE_NUCLEUS) ? 1 : 0;
+  a.nucleus_only = a.nucleus && (flags & PLH_SAMPLE_NUCLEUS_ONLY) ? 1 : 0;
   const bool f64 = dtype == PLH_F64;
   // the fast path gathers per-row state in LDS sized for V <= 262144
   if (out_probs != nullptr || (flags & PLH_SAMPLE_ROWWISE) || V > kMaxVBitmap) {

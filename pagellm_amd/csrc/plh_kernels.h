@@ -92,6 +92,8 @@ struct SampleArgs {
   double* out_probs;
   unsigned long long* fallback_rows;  // rows finished by the general path
   int nucleus;                        // 1: eligible rows take the nucleus path
+  int nucleus_only;                   // 1 (with nucleus): no merge launch; other rows take the
+                                      // general pipeline in k_nuc_final
   ChunkWs ws;                         // fast path only
 };
 

@@ -3086,7 +3086,16 @@ __global__ __launch_bounds__(kThreads) void k_nuc_final(SampleArgs a) {
   FastSmem& fs = sm.f;
   const int row = blockIdx.x;
   const RowParams rp = load_row_params(a, row);
-  if (!rp.nucleus) return;
+  if (!rp.nucleus) {
+    // with the nucleus-only hint no merge kernel ran: a row that is not a
+    // nucleus row is finished here
+    if (a.nucleus_only) {
+      if (threadIdx.x == 0) glb_add(a.fallback_rows, 1ull);
+      const int id = row_general<TIn, VEC>(a, row, rp, sm.g, nullptr);
+      if (threadIdx.x == 0) a.out_ids[row] = id;
+    }
+    return;
+  }
   const NucRow nr = a.ws.nrow[row];
   if (nr.state != kNucActive) return;
   init_exp_table_wave(fs.exp_tab[wave()]);
@@ -3427,7 +3436,10 @@ hipError_t launch_sample_fast(const SampleArgs& a, bool f64, bool vec, int num_c
     const hipError_t e = hipEventRecord(between, s);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(finals[f64][vec][nuc], gf, block, 0, s, a);
+  // every row a nucleus row (the caller's hint): they would all leave the
+  // merge kernel at once, so it is not launched (k_nuc_final finishes a row
+  // that is not one with the general pipeline)
+  if (!a.nucleus_only) hipLaunchKernelGGL(finals[f64][vec][nuc], gf, block, 0, s, a);
   if (a.nucleus) {
     auto cands = f64 ? (vec ? k_nuc_cands<double, true> : k_nuc_cands<double, false>)
                      : (vec ? k_nuc_cands<float, true> : k_nuc_cands<float, false>);

@@ -154,7 +154,10 @@ def _nucleus_hint(t: np.ndarray, k: np.ndarray, p: np.ndarray, V: int) -> int:
     which the multi-pass nucleus kernels handle faster than the per-row general
     pipeline.  The sampled ids do not depend on the hint."""
     rows = (t != 0) & ((k <= 0) | (k >= V)) & (p >= NUCLEUS_TOP_P) & (p < 1.0)
-    return _native.PLH_SAMPLE_NUCLEUS if bool(rows.any()) else 0
+    if not bool(rows.any()):
+        return 0
+    # every row one of them: no merge launch (PLH_SAMPLE_NUCLEUS_ONLY)
+    return _native.PLH_SAMPLE_NUCLEUS | (_native.PLH_SAMPLE_NUCLEUS_ONLY if bool(rows.all()) else 0)
 
 
 def _draw_uniforms(params, rngs, B: int) -> np.ndarray:

@@ -60,7 +60,7 @@ def test_status_codes_match_header():
     text = HEADER.read_text()
     for name in ["PLH_OK", "PLH_ERR_INVALID_ARG", "PLH_ERR_HIP", "PLH_ERR_OUT_OF_MEMORY", "PLH_ERR_UNSUPPORTED",
                  "PLH_ERR_NO_DEVICE", "PLH_F32", "PLH_F64", "PLH_SAMPLE_ROWWISE", "PLH_SAMPLE_HIST_SPANS", "PLH_SAMPLE_NUCLEUS",
-                 "PLH_OPT_KERNEL_TIMING"]:
+                 "PLH_SAMPLE_NUCLEUS_ONLY", "PLH_OPT_KERNEL_TIMING"]:
         m = re.search(rf"#define {name} (-?\d+)", text)
         assert m and int(m.group(1)) == getattr(_native, name), name
 

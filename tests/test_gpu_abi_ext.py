@@ -140,7 +140,8 @@ def test_nucleus_hint_changes_the_path_not_the_ids():
     from the general pipeline to the nucleus kernels: the same batch (a
     Zipf-like row set mixed with greedy, top-k and plain top-p rows, CSR and
     span histories) gives the same ids with and without it, and only
-    without it do the high-top_p rows fall back."""
+    without it do the high-top_p rows fall back.  PLH_SAMPLE_NUCLEUS_ONLY
+    (no merge launch) gives them too, right or wrong."""
     g = np.random.default_rng(8)
     B, V = 10, 60000
     ranks = 1 + np.stack([g.permutation(V) for _ in range(B)])
@@ -168,6 +169,22 @@ def test_nucleus_hint_changes_the_path_not_the_ids():
     for b in range(B):
         ref = oracle.sample(x[b], params[b], u[b], hists[b])
         assert hinted[b] == ref or min(oracle.sampler.sample_boundary_gaps(x[b], params[b], u[b], hists[b])) < DRAW_GAP
+    # PLH_SAMPLE_NUCLEUS_ONLY: no merge launch.  Given wrongly (the greedy,
+    # top-k and top_p 0.9 rows are not nucleus rows), those three rows are
+    # finished by the general pipeline in the nucleus path: the same ids
+    f3 = c.fallback_rows()
+    only = _sample(c, x, params, u, ids, off, _native.PLH_SAMPLE_NUCLEUS | _native.PLH_SAMPLE_NUCLEUS_ONLY)
+    f4 = c.fallback_rows()
+    assert np.array_equal(only, hinted)
+    assert f4 - f3 == 3, f4 - f3
+    # and given rightly, on the seven nucleus rows alone: the hinted ids
+    nuc = [b for b in range(B) if b < 6 or b == 9]
+    sub_ids = np.concatenate([hists[b] for b in nuc])
+    sub_off = np.concatenate([[0], np.cumsum([hists[b].size for b in nuc])]).astype(np.int64)
+    sub = _sample(c, x[nuc], [params[b] for b in nuc], u[nuc], sub_ids, sub_off,
+                  _native.PLH_SAMPLE_NUCLEUS | _native.PLH_SAMPLE_NUCLEUS_ONLY)
+    assert np.array_equal(sub, hinted[nuc])
+    assert c.fallback_rows() == f4
 
 
 def test_penalize_rejects_in_place_and_overlapping_output():

@@ -124,19 +124,21 @@ def test_bulk_uniform_draws_match_scalar_draws():
 
 def test_nucleus_hint_only_for_high_top_p_rows_without_top_k():
     """The hint is set when some non-greedy row has no top-k (0 or >= V) and
-    0.98 <= top_p < 1; it never depends on other rows."""
+    0.98 <= top_p < 1, with PLH_SAMPLE_NUCLEUS_ONLY when every row is one."""
     from pagellm_amd import _native
 
     def hint(rows, V=100):
         return S._nucleus_hint(*S._pack_params(rows)[:3], V)
 
-    assert hint([SamplingParams(top_p=0.99)]) == _native.PLH_SAMPLE_NUCLEUS
-    assert hint([SamplingParams(top_p=0.98, top_k=100)]) == _native.PLH_SAMPLE_NUCLEUS  # top_k >= V is off
+    both = _native.PLH_SAMPLE_NUCLEUS | _native.PLH_SAMPLE_NUCLEUS_ONLY
+    assert hint([SamplingParams(top_p=0.99)]) == both
+    assert hint([SamplingParams(top_p=0.98, top_k=100)]) == both  # top_k >= V is off
     assert hint([SamplingParams(top_p=0.97)]) == 0
     assert hint([SamplingParams(top_p=1.0)]) == 0
     assert hint([SamplingParams(top_p=0.99, top_k=40)]) == 0
     assert hint([SamplingParams(top_p=0.99, temperature=0.0)]) == 0
     assert hint([SamplingParams(), SamplingParams(top_p=0.995)]) == _native.PLH_SAMPLE_NUCLEUS
+    assert hint([SamplingParams(top_p=0.99), SamplingParams(top_p=0.995, temperature=0.7)]) == both
 
 
 def test_penalised_rows_beyond_the_bitmap_fail_on_the_host_with_the_reason():
