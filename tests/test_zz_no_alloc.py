@@ -56,6 +56,9 @@ def test_noalloc_matches_sample_on_two_calls_in_a_row():
         got_char = _call(c, workloads.char65(), True)
         assert np.array_equal(got_small2, ref_small)
         assert np.array_equal(got_char, _call(c, workloads.char65(), False))
+        # a batch of nucleus rows only (the nucleus kernels, no merge launch)
+        nuc = workloads.zipf152k(rows=8)
+        assert np.array_equal(_call(c, nuc, True), _call(c, nuc, False))
     finally:
         c.close()
 
