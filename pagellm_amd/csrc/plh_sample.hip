@@ -3086,18 +3086,15 @@ __global__ __launch_bounds__(kThreads) void k_nuc_final(SampleArgs a) {
   FastSmem& fs = sm.f;
   const int row = blockIdx.x;
   const RowParams rp = load_row_params(a, row);
-  if (!rp.nucleus) {
-    // with the nucleus-only hint no merge kernel ran: a row that is not a
-    // nucleus row is finished here
-    if (a.nucleus_only) {
-      if (threadIdx.x == 0) glb_add(a.fallback_rows, 1ull);
-      const int id = row_general<TIn, VEC>(a, row, rp, sm.g, nullptr);
-      if (threadIdx.x == 0) a.out_ids[row] = id;
-    }
-    return;
+  // with the nucleus-only hint no merge kernel ran: a row that is not a
+  // nucleus row is finished here, by the general pipeline below
+  const bool other = !rp.nucleus;
+  if (other && !a.nucleus_only) return;
+  NucRow nr{};
+  if (!other) {
+    nr = a.ws.nrow[row];
+    if (nr.state != kNucActive) return;
   }
-  const NucRow nr = a.ws.nrow[row];
-  if (nr.state != kNucActive) return;
   init_exp_table_wave(fs.exp_tab[wave()]);
   for (int b = threadIdx.x; b < kHB; b += kThreads) {  // ordered before use by the first barrier
     fs.h[0].cnt[b] = 0u;
@@ -3117,7 +3114,7 @@ __global__ __launch_bounds__(kThreads) void k_nuc_final(SampleArgs a) {
   const int csh = __ffs(capc) - 1;
   const int slots = C * capc;
   const int nseg = C * kWaves;
-  bool general = nr.general != 0;
+  bool general = other || nr.general != 0;
   int id = V - 1;
   if (!general) {
     // every candidate slot into registers; the chunks' counts per wave
